@@ -1,0 +1,689 @@
+// abi.hip — implementation of include/soklyn_hip.h.
+//
+// Each entry point validates its arguments the way the reference's
+// DenseBlock / GpuContext do (src/mlp.rs, src/io/device.rs) — that is also
+// what keeps every kernel launch inside the shapes it assumes — then issues
+// the MI355X kernels on the context's stream.
+#include <float.h>
+#include <math.h>
+#include <string.h>
+
+#include <hip/hip_runtime.h>
+
+#include "../../include/soklyn_hip.h"
+#include "launch.h"
+
+using namespace skl;
+
+struct skl_ctx {
+    int device;
+    uint32_t tile_dim;
+    hipStream_t own_stream;
+    hipStream_t stream;
+    uint32_t sync;
+    void *ws;
+    size_t ws_bytes;
+};
+
+namespace {
+
+int32_t hip_status(hipError_t e) { return e == hipSuccess ? SKL_OK : (int32_t)e; }
+
+#define SKL_TRY(expr)                                                  \
+    do {                                                               \
+        hipError_t _e = (expr);                                        \
+        if (_e != hipSuccess) return hip_status(_e);                   \
+    } while (0)
+
+#define SKL_CHECK(cond, code)                                          \
+    do {                                                               \
+        if (!(cond)) return (code);                                    \
+    } while (0)
+
+int32_t finish(skl_ctx *ctx) {
+    SKL_TRY(hipGetLastError());
+    if (ctx->sync) SKL_TRY(hipStreamSynchronize(ctx->stream));
+    return SKL_OK;
+}
+
+int32_t enter(skl_ctx *ctx) {
+    if (!ctx) return SKL_ERR_NULL_POINTER;
+    SKL_TRY(hipSetDevice(ctx->device));
+    return SKL_OK;
+}
+
+int32_t ensure_ws(skl_ctx *ctx, size_t bytes) {
+    if (bytes <= ctx->ws_bytes) return SKL_OK;
+    SKL_TRY(hipStreamSynchronize(ctx->stream));
+    if (ctx->ws) SKL_TRY(hipFree(ctx->ws));
+    ctx->ws = nullptr;
+    ctx->ws_bytes = 0;
+    size_t want = bytes + (bytes >> 3);
+    SKL_TRY(hipMalloc(&ctx->ws, want));
+    ctx->ws_bytes = want;
+    return SKL_OK;
+}
+
+size_t elem_size(uint32_t dtype) { return dtype == SKL_F16 ? 2 : 4; }
+
+// Common configuration checks of a block descriptor.
+int32_t check_desc(const skl_ctx *ctx, const skl_dense_desc *b) {
+    SKL_CHECK(b, SKL_ERR_NULL_POINTER);
+    SKL_CHECK(b->dtype <= SKL_F16, SKL_ERR_INVALID_CONFIGURATION);
+    SKL_CHECK(b->inputs > 0 && b->outputs > 0, SKL_ERR_INVALID_CONFIGURATION);   // mlp.rs:350-354
+    SKL_CHECK(b->max_batch > 0, SKL_ERR_INVALID_CONFIGURATION);                  // mlp.rs:356-360
+    SKL_CHECK(b->norm <= SKL_NORM_BATCH, SKL_ERR_INVALID_CONFIGURATION);
+    SKL_CHECK(b->act <= SKL_ACT_MISH, SKL_ERR_INVALID_CONFIGURATION);
+    SKL_CHECK(b->regularisation <= SKL_REGU_L2, SKL_ERR_INVALID_CONFIGURATION);
+    // check_tile_dim (device.rs:248-258)
+    SKL_CHECK(!(b->dtype == SKL_F16 && ctx->tile_dim != 16), SKL_ERR_HARDWARE_CONSTRAINT);
+    SKL_CHECK(b->w, SKL_ERR_NULL_POINTER);
+    return SKL_OK;
+}
+
+// check_input_dimension (mlp.rs:492-519)
+int32_t check_input(const skl_dense_desc *b, const void *in, uint32_t in_rows, uint32_t in_cols, uint32_t batch) {
+    SKL_CHECK(in, SKL_ERR_NULL_POINTER);
+    SKL_CHECK(in_rows >= batch, SKL_ERR_MISMATCHED_DIMENSIONS);
+    SKL_CHECK(in_rows <= b->max_batch, SKL_ERR_ALLOCATION_LIMIT);
+    SKL_CHECK(in_cols == b->inputs, SKL_ERR_MISMATCHED_DIMENSIONS);
+    return SKL_OK;
+}
+
+// Softmax / batch-size checks shared by forward and the backward calls
+// (mlp.rs:558-575, 620-639, 710-726).
+int32_t check_act_batch(const skl_dense_desc *b, uint32_t batch) {
+    SKL_CHECK(b->act != SKL_ACT_SOFTMAX, SKL_ERR_INVALID_CONFIGURATION);
+    SKL_CHECK(batch > 0, SKL_ERR_INVALID_BATCH_SIZE);
+    SKL_CHECK(!(b->norm == SKL_NORM_BATCH && batch == 1), SKL_ERR_INVALID_BATCH_SIZE);
+    return SKL_OK;
+}
+
+int32_t check_norm_cache(const skl_dense_desc *b) {
+    if (b->norm == SKL_NORM_DISABLED) return SKL_OK;
+    SKL_CHECK(b->prenorm && b->centered && b->norm_rstd && b->norm_w && b->norm_b, SKL_ERR_NULL_POINTER);
+    return SKL_OK;
+}
+
+int32_t check_backward_buffers(const skl_dense_desc *b) {
+    SKL_CHECK(b->grad && b->d_prenorm, SKL_ERR_NULL_POINTER);
+    if (b->dtype == SKL_F16) SKL_CHECK(b->d_prenorm_h, SKL_ERR_NULL_POINTER);
+    if (b->norm != SKL_NORM_DISABLED) SKL_CHECK(b->d_norm_w && b->d_norm_b, SKL_ERR_NULL_POINTER);
+    return check_norm_cache(b);
+}
+
+const float *master_norm_w(const skl_dense_desc *b) {
+    return b->dtype == SKL_F16 ? b->master_norm_w : reinterpret_cast<const float *>(b->norm_w);
+}
+
+OptParams opt_params(const skl_optimiser &o, uint32_t step) {
+    OptParams p;
+    p.kind = o.kind;
+    p.beta1 = o.beta1;
+    p.beta2 = o.beta2;
+    p.epsilon = o.epsilon;
+    p.nesterov = o.nesterov;
+    // backward.cu:141-142 (powf(beta, step)); step 0 divides by zero there too
+    p.bc1 = 1.0f - powf(o.beta1, (float)step);
+    p.bc2 = 1.0f - powf(o.beta2, (float)step);
+    return p;
+}
+
+// The reference zero-fills dNorm before every backward kernel
+// (ffn_device.rs:148-149, 370-371) and the kernels then write rows [0, rows).
+// Only the rows no kernel writes need the fill.  With norm Disabled the
+// buffers are never written at all (they keep the zeros of allocation,
+// mlp.rs:404-410), so nothing is launched.
+int32_t zero_dnorm_tail(skl_ctx *ctx, const skl_dense_desc *b, uint32_t rows_written) {
+    if (b->norm == SKL_NORM_DISABLED || rows_written >= b->max_batch) return SKL_OK;
+    const size_t off = (size_t)rows_written * b->outputs;
+    const size_t n = (size_t)(b->max_batch - rows_written) * b->outputs;
+    SKL_TRY(launch_fill(b->d_norm_w + off, SKL_F32, 0.0f, n, ctx->stream));
+    SKL_TRY(launch_fill(b->d_norm_b + off, SKL_F32, 0.0f, n, ctx->stream));
+    return SKL_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *skl_status_string(int32_t s) {
+    switch (s) {
+    case SKL_OK: return "ok";
+    case SKL_ERR_INVALID_CONFIGURATION: return "invalid configuration";
+    case SKL_ERR_TRAINING_MODE_REQUIRED: return "training mode required";
+    case SKL_ERR_ALLOCATION_LIMIT: return "allocation limit exceeded";
+    case SKL_ERR_MISMATCHED_DIMENSIONS: return "mismatched dimensions";
+    case SKL_ERR_INVALID_BATCH_SIZE: return "invalid batch size";
+    case SKL_ERR_HARDWARE_CONSTRAINT: return "hardware constraint violation (fp16 requires tile_dim 16)";
+    case SKL_ERR_TRY_FROM_INT: return "integer conversion overflow";
+    case SKL_ERR_NULL_POINTER: return "required pointer is null";
+    case SKL_ERR_UNSUPPORTED_CAST: return "unsupported precision cast";
+    case SKL_ERR_NO_DEVICE: return "no usable device";
+    default: return s > 0 ? hipGetErrorString((hipError_t)s) : "unknown status";
+    }
+}
+
+int32_t skl_ctx_create(int32_t ordinal, uint32_t tile_dim, skl_ctx **out) {
+    if (!out) return SKL_ERR_NULL_POINTER;
+    *out = nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || ordinal < 0 || ordinal >= count) return SKL_ERR_NO_DEVICE;
+    if (tile_dim == 0) return SKL_ERR_INVALID_CONFIGURATION;
+    SKL_TRY(hipSetDevice(ordinal));
+    skl_ctx *c = new skl_ctx();
+    c->device = ordinal;
+    c->tile_dim = tile_dim;
+    c->sync = 1;
+    c->ws = nullptr;
+    c->ws_bytes = 0;
+    hipError_t e = hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete c;
+        return hip_status(e);
+    }
+    c->stream = c->own_stream;
+    *out = c;
+    return SKL_OK;
+}
+
+int32_t skl_ctx_destroy(skl_ctx *ctx) {
+    if (!ctx) return SKL_ERR_NULL_POINTER;
+    hipSetDevice(ctx->device);
+    hipStreamSynchronize(ctx->stream);
+    if (ctx->ws) hipFree(ctx->ws);
+    hipStreamDestroy(ctx->own_stream);
+    delete ctx;
+    return SKL_OK;
+}
+
+int32_t skl_ctx_set_sync(skl_ctx *ctx, uint32_t sync_each_call) {
+    if (!ctx) return SKL_ERR_NULL_POINTER;
+    ctx->sync = sync_each_call ? 1 : 0;
+    return SKL_OK;
+}
+
+int32_t skl_ctx_set_stream(skl_ctx *ctx, void *hip_stream) {
+    if (!ctx) return SKL_ERR_NULL_POINTER;
+    ctx->stream = hip_stream ? reinterpret_cast<hipStream_t>(hip_stream) : ctx->own_stream;
+    return SKL_OK;
+}
+
+void *skl_ctx_stream(skl_ctx *ctx) { return ctx ? reinterpret_cast<void *>(ctx->stream) : nullptr; }
+
+int32_t skl_synchronize(skl_ctx *ctx) {
+    int32_t r = enter(ctx);
+    if (r) return r;
+    SKL_TRY(hipStreamSynchronize(ctx->stream));
+    return SKL_OK;
+}
+
+int32_t skl_malloc(skl_ctx *ctx, void **ptr, size_t bytes) {
+    int32_t r = enter(ctx);
+    if (r) return r;
+    if (!ptr) return SKL_ERR_NULL_POINTER;
+    *ptr = nullptr;
+    SKL_TRY(hipMalloc(ptr, bytes ? bytes : 1));
+    return SKL_OK;
+}
+
+int32_t skl_free(skl_ctx *ctx, void *ptr) {
+    int32_t r = enter(ctx);
+    if (r) return r;
+    if (!ptr) return SKL_OK;
+    SKL_TRY(hipStreamSynchronize(ctx->stream));
+    SKL_TRY(hipFree(ptr));
+    return SKL_OK;
+}
+
+static int32_t copy(skl_ctx *ctx, void *dst, const void *src, size_t bytes, hipMemcpyKind kind) {
+    int32_t r = enter(ctx);
+    if (r) return r;
+    if (bytes == 0) return SKL_OK;
+    if (!dst || !src) return SKL_ERR_NULL_POINTER;
+    SKL_TRY(hipMemcpyAsync(dst, src, bytes, kind, ctx->stream));
+    SKL_TRY(hipStreamSynchronize(ctx->stream));
+    return SKL_OK;
+}
+
+int32_t skl_memcpy_h2d(skl_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    return copy(ctx, dst, src, bytes, hipMemcpyHostToDevice);
+}
+int32_t skl_memcpy_d2h(skl_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    return copy(ctx, dst, src, bytes, hipMemcpyDeviceToHost);
+}
+int32_t skl_memcpy_d2d(skl_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    return copy(ctx, dst, src, bytes, hipMemcpyDeviceToDevice);
+}
+
+int32_t skl_fill(skl_ctx *ctx, void *dst, uint32_t dtype, float v, size_t n) {
+    int32_t r = enter(ctx);
+    if (r) return r;
+    if (dtype > SKL_F16) return SKL_ERR_INVALID_CONFIGURATION;
+    if (n && !dst) return SKL_ERR_NULL_POINTER;
+    SKL_TRY(launch_fill(dst, dtype, v, n, ctx->stream));
+    return finish(ctx);
+}
+
+int32_t skl_cast(skl_ctx *ctx, const void *src, uint32_t sdt, void *dst, uint32_t ddt, size_t n) {
+    int32_t r = enter(ctx);
+    if (r) return r;
+    if (sdt > SKL_F16 || ddt > SKL_F16) return SKL_ERR_UNSUPPORTED_CAST;
+    if (n && (!src || !dst)) return SKL_ERR_NULL_POINTER;
+    SKL_TRY(launch_cast(src, sdt, dst, ddt, n, ctx->stream));
+    return finish(ctx);
+}
+
+uint32_t skl_scramble_seed(uint32_t step, uint32_t layer_id) {
+    uint32_t h = step * 1103515245u + layer_id;
+    h = (h ^ (h >> 16)) * 1103515245u;
+    return h ^ (h >> 15);
+}
+
+int32_t skl_dense_forward(skl_ctx *ctx, const skl_dense_desc *b, const void *in, uint32_t in_rows,
+                          uint32_t in_cols, uint32_t batch, uint32_t use_dropout, uint32_t seed) {
+    int32_t r = enter(ctx);
+    if (r) return r;
+    if ((r = check_desc(ctx, b))) return r;
+    if ((r = check_input(b, in, in_rows, in_cols, batch))) return r;
+    if ((r = check_act_batch(b, batch))) return r;
+    if ((r = check_norm_cache(b))) return r;
+    SKL_CHECK(b->out && b->predrop && b->preact, SKL_ERR_NULL_POINTER);
+    const bool use_bias = b->norm != SKL_NORM_BATCH;   // ffn_device.rs:30
+    SKL_CHECK(!use_bias || b->b, SKL_ERR_NULL_POINTER);
+    SKL_CHECK(!use_dropout || b->mask, SKL_ERR_NULL_POINTER);
+
+    GemmLaunch g{};
+    g.dtype = b->dtype;
+    g.M = batch;
+    g.N = b->outputs;
+    g.K = b->inputs;
+    g.lda = in_cols;
+    g.ldb = b->outputs;
+    g.a_kcontig = true;
+    g.b_kcontig = false;
+    g.A = in;
+    g.B = b->w;
+    g.splits = 1;
+    g.op = Op::Fwd;
+    g.fwd.bias = use_bias ? b->b : nullptr;
+    g.fwd.z_out = b->norm == SKL_NORM_DISABLED ? b->preact : b->prenorm;   // ffn_device.rs:51-55
+    g.fwd.predrop = b->predrop;
+    g.fwd.out = b->out;
+    g.fwd.mask = b->mask;
+    g.fwd.fuse_act = b->norm == SKL_NORM_DISABLED;
+    g.fwd.act = b->act;
+    g.fwd.use_dropout = use_dropout ? 1 : 0;
+    g.fwd.seed = seed;
+    g.fwd.leaky = b->act == SKL_ACT_LEAKY_RELU ? b->leaky : 0.0f;       // ffn_device.rs:32-35
+    g.fwd.p = b->mask_coeff;
+    g.fwd.ldc = b->outputs;
+    SKL_TRY(launch_gemm(g, ctx->stream));
+
+    if (b->norm != SKL_NORM_DISABLED) {
+        RowNormArgs a{};
+        a.dtype = b->dtype;
+        a.m = batch;
+        a.n = b->outputs;
+        a.norm = b->norm;
+        a.act = b->act;
+        a.use_dropout = use_dropout ? 1 : 0;
+        a.seed = seed;
+        a.leaky = g.fwd.leaky;
+        a.p = b->mask_coeff;
+        a.prenorm = b->prenorm;
+        a.norm_w = b->norm_w;
+        a.norm_b = b->norm_b;
+        a.centered = b->centered;
+        a.preact = b->preact;
+        a.predrop = b->predrop;
+        a.out = b->out;
+        a.mask = b->mask;
+        a.norm_rstd = b->norm_rstd;
+        SKL_TRY(launch_norm_act(a, ctx->stream));
+    }
+    return finish(ctx);
+}
+
+int32_t skl_dense_output_error(skl_ctx *ctx, const skl_dense_desc *b, const void *target, uint32_t target_rows,
+                               uint32_t target_cols, uint32_t loss, uint32_t act, float leaky) {
+    int32_t r = enter(ctx);
+    if (r) return r;
+    if ((r = check_desc(ctx, b))) return r;
+    // compute_loss (mlp.rs:756-821)
+    SKL_CHECK(b->is_training, SKL_ERR_TRAINING_MODE_REQUIRED);
+    SKL_CHECK(target, SKL_ERR_NULL_POINTER);
+    SKL_CHECK(target_cols == b->outputs, SKL_ERR_MISMATCHED_DIMENSIONS);
+    SKL_CHECK(target_rows <= b->max_batch, SKL_ERR_ALLOCATION_LIMIT);
+    SKL_CHECK(loss <= SKL_LOSS_BCE && act <= SKL_ACT_MISH, SKL_ERR_INVALID_CONFIGURATION);
+    if (loss == SKL_LOSS_MSE) SKL_CHECK(act != SKL_ACT_SOFTMAX, SKL_ERR_INVALID_CONFIGURATION);
+    if (loss == SKL_LOSS_CE) SKL_CHECK(act == SKL_ACT_SOFTMAX, SKL_ERR_INVALID_CONFIGURATION);
+    if (loss == SKL_LOSS_BCE) SKL_CHECK(act == SKL_ACT_SIGMOID, SKL_ERR_INVALID_CONFIGURATION);
+    if ((r = check_backward_buffers(b))) return r;
+    SKL_CHECK(b->out && b->preact, SKL_ERR_NULL_POINTER);
+    if (b->dtype == SKL_F16 && b->norm) SKL_CHECK(b->master_norm_w, SKL_ERR_NULL_POINTER);
+
+    // The reference zero-fills all dNorm rows, then writes rows [0, m).
+    if ((r = zero_dnorm_tail(ctx, b, target_rows))) return r;
+    // Softmax in place on out over all cache rows (ffn_device.rs:167-186).
+    if (act == SKL_ACT_SOFTMAX) SKL_TRY(launch_softmax(b->dtype, b->out, b->max_batch, b->outputs, ctx->stream));
+
+    ErrArgs a{};
+    a.dtype = b->dtype;
+    a.rows = target_rows;   // kernel m = max_batch (Q: ffn_device.rs:152); rows past target_rows are not readable
+    a.n = b->outputs;
+    a.norm = b->norm;
+    a.act = act;
+    a.loss = loss;
+    a.leaky = act == SKL_ACT_LEAKY_RELU ? leaky : 0.0f;
+    a.inv_n = 1.0f / (float)b->outputs;
+    a.inv_m = 1.0f / (float)b->max_batch;
+    a.loss_scale = 512.0f;
+    a.out = b->out;
+    a.preact = b->preact;
+    a.target = target;
+    a.norm_rstd = b->norm_rstd;
+    a.centered = b->centered;
+    a.prenorm = b->prenorm;
+    a.nw = master_norm_w(b);
+    a.grad = b->grad;
+    a.d_prenorm = b->d_prenorm;
+    a.d_norm_w = b->d_norm_w;
+    a.d_norm_b = b->d_norm_b;
+    a.d_prenorm_h = b->dtype == SKL_F16 ? reinterpret_cast<half_t *>(b->d_prenorm_h) : nullptr;
+    SKL_TRY(launch_output_error(a, ctx->stream));
+    return finish(ctx);
+}
+
+static int32_t hidden_error_impl(skl_ctx *ctx, const skl_dense_desc *cur, const skl_dense_desc *next,
+                                 uint32_t batch) {
+    int32_t r;
+    if ((r = check_desc(ctx, cur))) return r;
+    if ((r = check_desc(ctx, next))) return r;
+    SKL_CHECK(cur->dtype == next->dtype, SKL_ERR_INVALID_CONFIGURATION);
+    SKL_CHECK(cur->is_training, SKL_ERR_TRAINING_MODE_REQUIRED);                 // mlp.rs:682-686
+    SKL_CHECK(next->inputs == cur->outputs, SKL_ERR_MISMATCHED_DIMENSIONS);      // mlp.rs:690-697
+    SKL_CHECK(batch <= cur->max_batch, SKL_ERR_ALLOCATION_LIMIT);
+    SKL_CHECK(next->max_batch >= batch, SKL_ERR_MISMATCHED_DIMENSIONS);          // mlp.rs:699-706
+    if ((r = check_act_batch(cur, batch))) return r;
+    if ((r = check_backward_buffers(cur))) return r;
+    SKL_CHECK(cur->predrop && cur->preact && cur->mask, SKL_ERR_NULL_POINTER);
+    SKL_CHECK(next->d_prenorm, SKL_ERR_NULL_POINTER);
+    if (cur->dtype == SKL_F16) {
+        SKL_CHECK(next->d_prenorm_h, SKL_ERR_NULL_POINTER);
+        if (cur->norm) SKL_CHECK(cur->master_norm_w, SKL_ERR_NULL_POINTER);
+    }
+    if ((r = zero_dnorm_tail(ctx, cur, batch))) return r;
+
+    GemmLaunch g{};
+    g.dtype = cur->dtype;
+    g.M = batch;
+    g.N = cur->outputs;
+    g.K = next->outputs;
+    g.lda = next->outputs;
+    g.ldb = next->outputs;
+    g.a_kcontig = true;
+    g.b_kcontig = true;
+    // fp16: f16(d_prenorm) and the working W (== f16(master) after every update)
+    g.A = cur->dtype == SKL_F16 ? next->d_prenorm_h : next->d_prenorm;
+    g.B = next->w;
+    g.splits = 1;
+    g.op = Op::Hidden;
+    HiddenEpi &h = g.hid;
+    h.predrop = cur->predrop;
+    h.preact = cur->preact;
+    h.mask = cur->mask;
+    h.norm_rstd = cur->norm_rstd;
+    h.centered = cur->centered;
+    h.prenorm = cur->prenorm;
+    h.nw = master_norm_w(cur);
+    h.grad = cur->grad;
+    h.d_prenorm = cur->d_prenorm;
+    h.d_norm_w = cur->d_norm_w;
+    h.d_norm_b = cur->d_norm_b;
+    h.d_prenorm_h = cur->dtype == SKL_F16 ? reinterpret_cast<half_t *>(cur->d_prenorm_h) : nullptr;
+    h.norm = cur->norm;
+    h.act = cur->act;
+    h.leaky = cur->act == SKL_ACT_LEAKY_RELU ? cur->leaky : 0.0f;
+    h.inv_n = 1.0f / (float)cur->outputs;
+    h.inv_m = 1.0f / (float)batch;
+    h.loss_scale = 1.0f;
+    h.ldc = cur->outputs;
+    SKL_TRY(launch_gemm(g, ctx->stream));
+    return SKL_OK;
+}
+
+int32_t skl_dense_hidden_error(skl_ctx *ctx, const skl_dense_desc *cur, const skl_dense_desc *next,
+                               uint32_t batch) {
+    int32_t r = enter(ctx);
+    if (r) return r;
+    if ((r = hidden_error_impl(ctx, cur, next, batch))) return r;
+    return finish(ctx);
+}
+
+static int32_t backward_impl(skl_ctx *ctx, const skl_dense_desc *b, const void *in, uint32_t in_rows,
+                             uint32_t in_cols, const skl_train_ctx *t, uint32_t step) {
+    int32_t r;
+    if ((r = check_desc(ctx, b))) return r;
+    SKL_CHECK(t, SKL_ERR_NULL_POINTER);
+    SKL_CHECK(b->is_training, SKL_ERR_TRAINING_MODE_REQUIRED);                   // mlp.rs:614-618
+    const uint32_t batch = t->batch_size;
+    if ((r = check_input(b, in, in_rows, in_cols, batch))) return r;
+    if ((r = check_act_batch(b, batch))) return r;
+    if ((r = check_backward_buffers(b))) return r;
+    SKL_CHECK(t->optimiser.kind <= SKL_OPT_ADAM && t->norm_optimiser.kind <= SKL_OPT_ADAM,
+              SKL_ERR_INVALID_CONFIGURATION);
+    const bool use_bias = b->norm != SKL_NORM_BATCH;   // ffn_device.rs:245
+    const bool f16 = b->dtype == SKL_F16;
+    SKL_CHECK(b->dv_w && b->dm_w, SKL_ERR_NULL_POINTER);
+    if (f16) SKL_CHECK(b->master_w, SKL_ERR_NULL_POINTER);
+    if (use_bias) {
+        SKL_CHECK(b->b && b->dv_b && b->dm_b, SKL_ERR_NULL_POINTER);
+        if (f16) SKL_CHECK(b->master_b, SKL_ERR_NULL_POINTER);
+    }
+    if (b->norm) {
+        SKL_CHECK(b->dv_norm_w && b->dm_norm_w, SKL_ERR_NULL_POINTER);
+        if (f16) SKL_CHECK(b->master_norm_w, SKL_ERR_NULL_POINTER);
+        if (b->norm > 1) {
+            SKL_CHECK(b->dv_norm_b && b->dm_norm_b, SKL_ERR_NULL_POINTER);
+            if (f16) SKL_CHECK(b->master_norm_b, SKL_ERR_NULL_POINTER);
+        }
+    }
+
+    const float inv_m = 1.0f / (float)batch;
+    const uint32_t K = b->inputs, N = b->outputs;
+
+    // -- dW = in^T . dP, fused with the optimiser step on W ----------------------------
+    OptEpi oe{};
+    oe.master = f16 ? b->master_w : reinterpret_cast<float *>(b->w);   // device.rs:262-272
+    oe.param = f16 ? b->w : nullptr;
+    oe.dv = b->dv_w;
+    oe.dm = b->dm_w;
+    oe.opt = opt_params(t->optimiser, step);
+    oe.lr = t->learn_rate;
+    oe.clamp = t->grad_clamp;
+    oe.inv_m = inv_m;
+    oe.regu_coeff = b->regularisation ? b->regu_coeff : 0.0f;
+    oe.regularisation = b->regularisation;
+    oe.ldc = N;
+
+    const uint32_t tiles = gemm_tiles(b->dtype, K, N);
+    const uint32_t bk = gemm_bk(b->dtype);
+    uint32_t splits = 1;
+    if (tiles < 160 && batch >= 8 * bk) {
+        splits = (256 + tiles - 1) / tiles;
+        const uint32_t max_splits = batch / (4 * bk);
+        if (splits > max_splits) splits = max_splits;
+        if (splits > 16) splits = 16;
+        if (splits < 2) splits = 1;
+    }
+
+    // column partial sums for db / dNorm sums share the workspace
+    const uint32_t col_blocks = (N + 255) / 256;
+    uint32_t csplits = (1024 + col_blocks - 1) / col_blocks;
+    const uint32_t cmax = batch / 32 > 0 ? batch / 32 : 1;
+    if (csplits > cmax) csplits = cmax;
+    if (csplits > 256) csplits = 256;
+    if (csplits < 1) csplits = 1;
+
+    const size_t dw_bytes = splits > 1 ? (size_t)splits * K * N * sizeof(float) : 0;
+    const size_t col_bytes = (size_t)csplits * 3 * N * sizeof(float);
+    if ((r = ensure_ws(ctx, dw_bytes + col_bytes))) return r;
+    float *ws_dw = reinterpret_cast<float *>(ctx->ws);
+    float *ws_col = reinterpret_cast<float *>(reinterpret_cast<char *>(ctx->ws) + dw_bytes);
+
+    GemmLaunch g{};
+    g.dtype = b->dtype;
+    g.M = K;
+    g.N = N;
+    g.K = batch;
+    g.lda = in_cols;
+    g.ldb = N;
+    g.a_kcontig = false;
+    g.b_kcontig = false;
+    g.A = in;
+    g.B = f16 ? b->d_prenorm_h : b->d_prenorm;
+    g.splits = splits;
+    if (splits == 1) {
+        g.op = Op::DwOpt;
+        g.opt = oe;
+        SKL_TRY(launch_gemm(g, ctx->stream));
+    } else {
+        g.op = Op::DwPartial;
+        g.st.out = ws_dw;
+        g.st.split_stride = (uint64_t)K * N;
+        g.st.ldc = N;
+        SKL_TRY(launch_gemm(g, ctx->stream));
+        DwReduceArgs d{};
+        d.dtype = b->dtype;
+        d.rows = K;
+        d.n = N;
+        d.splits = splits;
+        d.partials = ws_dw;
+        d.e = oe;
+        SKL_TRY(launch_dw_reduce_opt(d, ctx->stream));
+    }
+
+    // -- db, sum dNorm_w, sum dNorm_b and their optimiser steps -----------------------
+    VecOptArgs v{};
+    v.dtype = b->dtype;
+    v.rows = batch;
+    v.n = N;
+    v.splits = csplits;
+    v.src[0] = use_bias ? b->d_prenorm : nullptr;
+    v.src[1] = b->norm > 0 ? b->d_norm_w : nullptr;
+    v.src[2] = b->norm > 1 ? b->d_norm_b : nullptr;
+    v.partials = ws_col;
+    void *params[3] = {b->b, b->norm_w, b->norm_b};
+    float *masters[3] = {b->master_b, b->master_norm_w, b->master_norm_b};
+    float *dvs[3] = {b->dv_b, b->dv_norm_w, b->dv_norm_b};
+    float *dms[3] = {b->dm_b, b->dm_norm_w, b->dm_norm_b};
+    for (int k = 0; k < 3; ++k) {
+        v.enabled[k] = v.src[k] != nullptr;
+        v.param[k] = f16 ? params[k] : nullptr;
+        v.master[k] = f16 ? masters[k] : reinterpret_cast<float *>(params[k]);
+        v.dv[k] = dvs[k];
+        v.dm[k] = dms[k];
+        v.opt[k] = opt_params(k == 0 ? t->optimiser : t->norm_optimiser, step);
+    }
+    v.lr = t->learn_rate;
+    v.clamp = t->grad_clamp;
+    v.inv_m = inv_m;
+    if (v.enabled[0] || v.enabled[1] || v.enabled[2]) {
+        SKL_TRY(launch_colsum(v, ctx->stream));
+        SKL_TRY(launch_vec_opt(v, ctx->stream));
+    }
+    return SKL_OK;
+}
+
+int32_t skl_dense_backward(skl_ctx *ctx, const skl_dense_desc *b, const void *in, uint32_t in_rows,
+                           uint32_t in_cols, const skl_train_ctx *t, uint32_t step) {
+    int32_t r = enter(ctx);
+    if (r) return r;
+    if ((r = backward_impl(ctx, b, in, in_rows, in_cols, t, step))) return r;
+    return finish(ctx);
+}
+
+int32_t skl_dense_backward_hidden(skl_ctx *ctx, const skl_dense_desc *cur, const skl_dense_desc *next,
+                                  const void *in, uint32_t in_rows, uint32_t in_cols, const skl_train_ctx *t,
+                                  uint32_t step) {
+    int32_t r = enter(ctx);
+    if (r) return r;
+    SKL_CHECK(t, SKL_ERR_NULL_POINTER);
+    if ((r = check_desc(ctx, cur))) return r;
+    SKL_CHECK(cur->is_training, SKL_ERR_TRAINING_MODE_REQUIRED);
+    if ((r = check_input(cur, in, in_rows, in_cols, t->batch_size))) return r;
+    if ((r = hidden_error_impl(ctx, cur, next, t->batch_size))) return r;
+    if ((r = backward_impl(ctx, cur, in, in_rows, in_cols, t, step))) return r;
+    return finish(ctx);
+}
+
+int32_t skl_dense_error_from_sum(skl_ctx *ctx, const skl_dense_desc *b, const float *s, uint32_t batch) {
+    int32_t r = enter(ctx);
+    if (r) return r;
+    if ((r = check_desc(ctx, b))) return r;
+    SKL_CHECK(b->is_training, SKL_ERR_TRAINING_MODE_REQUIRED);
+    SKL_CHECK(s, SKL_ERR_NULL_POINTER);
+    SKL_CHECK(batch <= b->max_batch, SKL_ERR_ALLOCATION_LIMIT);
+    if ((r = check_act_batch(b, batch))) return r;
+    if ((r = check_backward_buffers(b))) return r;
+    SKL_CHECK(b->predrop && b->preact && b->mask, SKL_ERR_NULL_POINTER);
+    if (b->dtype == SKL_F16 && b->norm) SKL_CHECK(b->master_norm_w, SKL_ERR_NULL_POINTER);
+    if ((r = zero_dnorm_tail(ctx, b, batch))) return r;
+    ErrArgs a{};
+    a.dtype = b->dtype;
+    a.rows = batch;
+    a.n = b->outputs;
+    a.norm = b->norm;
+    a.act = b->act;
+    a.leaky = b->act == SKL_ACT_LEAKY_RELU ? b->leaky : 0.0f;
+    a.inv_n = 1.0f / (float)b->outputs;
+    a.inv_m = 1.0f / (float)batch;
+    a.loss_scale = 1.0f;
+    a.s = s;
+    a.predrop = b->predrop;
+    a.preact = b->preact;
+    a.mask = b->mask;
+    a.norm_rstd = b->norm_rstd;
+    a.centered = b->centered;
+    a.prenorm = b->prenorm;
+    a.nw = master_norm_w(b);
+    a.grad = b->grad;
+    a.d_prenorm = b->d_prenorm;
+    a.d_norm_w = b->d_norm_w;
+    a.d_norm_b = b->d_norm_b;
+    a.d_prenorm_h = b->dtype == SKL_F16 ? reinterpret_cast<half_t *>(b->d_prenorm_h) : nullptr;
+    SKL_TRY(launch_error_from_sum(a, ctx->stream));
+    return finish(ctx);
+}
+
+int32_t skl_dense_input_grad(skl_ctx *ctx, const skl_dense_desc *b, uint32_t batch, float *dx) {
+    int32_t r = enter(ctx);
+    if (r) return r;
+    if ((r = check_desc(ctx, b))) return r;
+    SKL_CHECK(dx, SKL_ERR_NULL_POINTER);
+    SKL_CHECK(batch > 0, SKL_ERR_INVALID_BATCH_SIZE);
+    SKL_CHECK(batch <= b->max_batch, SKL_ERR_ALLOCATION_LIMIT);
+    const bool f16 = b->dtype == SKL_F16;
+    SKL_CHECK(f16 ? b->d_prenorm_h != nullptr : b->d_prenorm != nullptr, SKL_ERR_NULL_POINTER);
+    GemmLaunch g{};
+    g.dtype = b->dtype;
+    g.M = batch;
+    g.N = b->inputs;
+    g.K = b->outputs;
+    g.lda = b->outputs;
+    g.ldb = b->outputs;
+    g.a_kcontig = true;
+    g.b_kcontig = true;
+    g.A = f16 ? b->d_prenorm_h : b->d_prenorm;
+    g.B = b->w;
+    g.splits = 1;
+    g.op = Op::InputGrad;
+    g.st.out = dx;
+    g.st.split_stride = 0;
+    g.st.ldc = b->inputs;
+    SKL_TRY(launch_gemm(g, ctx->stream));
+    return finish(ctx);
+}
+
+}  // extern "C"

@@ -1,0 +1,139 @@
+// device_math.h — element-level device functions of the DenseBlock hot path
+// (gfx950).  Each restates the reference function cited beside it.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace skl {
+
+typedef _Float16 half_t;
+
+// Element type of T tensors.
+template <typename T> struct TypeTag;
+template <> struct TypeTag<float> { static constexpr uint32_t code = 0; };
+template <> struct TypeTag<half_t> { static constexpr uint32_t code = 1; };
+
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(half_t v) { return (float)v; }
+template <typename T> __device__ __forceinline__ T from_f32(float v) { return (T)v; }  // RNE
+
+constexpr float kLossScale = 512.0f;            // backward.cu:8
+constexpr float kLossScaleInv = 1.0f / 512.0f;  // backward.cu:9
+
+// util.cu:8-47
+__device__ __forceinline__ float activation(uint32_t act, float x, float leaky) {
+    switch (act) {
+    case 1: return 1.0f / (1.0f + expf(-x));
+    case 2: return fmaxf(0.0f, x);
+    case 3: return x > 0.0f ? x : leaky * x;
+    case 4: return tanhf(x);
+    case 6: return x / (1.0f + expf(-x));
+    case 7: {
+        const float e_x = expf(x);
+        const float sp = x > 20.0f ? x : logf(1.0f + e_x);   // softplus with the reference cutoff
+        const float e_sp = expf(sp);
+        const float e_sp_inv = 1.0f / e_sp;
+        return x * ((e_sp - e_sp_inv) / (e_sp + e_sp_inv));
+    }
+    default: return x;
+    }
+}
+
+// util.cu:49-93 (ReLU / LeakyReLU test the post-activation value out_v)
+__device__ __forceinline__ float activation_derivative(uint32_t act, float err, float out_v, float in_x,
+                                                       float leaky) {
+    switch (act) {
+    case 1: return err * (out_v * (1.0f - out_v));
+    case 2: return err * (out_v > 0.0f ? 1.0f : 0.0f);
+    case 3: return err * (out_v > 0.0f ? 1.0f : leaky);
+    case 4: return err * (1.0f - out_v * out_v);
+    case 6: {
+        const float sig = 1.0f / (1.0f + expf(-in_x));
+        return err * (sig + out_v * (1.0f - sig));
+    }
+    case 7: {
+        const float e_x = expf(in_x);
+        const float sp = in_x > 20.0f ? in_x : logf(1.0f + e_x);
+        const float e_sp = expf(sp);
+        const float e_sp_inv = 1.0f / e_sp;
+        const float t = (e_sp - e_sp_inv) / (e_sp + e_sp_inv);
+        const float sig = e_x / (1.0f + e_x);
+        return err * (t + in_x * sig * (1.0f - t * t));
+    }
+    default: return err;
+    }
+}
+
+// math.cuh:45-53.  The 64-bit product col * 6364136223846793005 keeps only its
+// low 32 bits in the 32-bit state, i.e. col * 0x4C957F2D mod 2^32.
+__device__ __forceinline__ float dropout_u(uint32_t col, uint32_t row, uint32_t seed) {
+    uint32_t s = (row * 1103515245u) ^ (col * 0x4C957F2Du) ^ seed;
+    s = s ^ (s >> 17);
+    s = s * 1103515245u + 12345u;
+    s = s ^ (s >> 15);
+    return (float)s / 4294967296.0f;
+}
+
+// util.cu:175-215 — element-local norm gradient.
+struct NormGrad {
+    float d_prenorm, dnw, dnb;
+};
+__device__ __forceinline__ NormGrad norm_grad(uint32_t norm, float e, float prenorm_v, float centered_v,
+                                              float rstd, float nw, float inv_n, float inv_m) {
+    NormGrad g{e, 0.0f, 0.0f};
+    if (norm == 1) {
+        g.dnw = e * prenorm_v * rstd;
+        g.d_prenorm = nw * rstd * (e - rstd * rstd * prenorm_v * prenorm_v * inv_n);
+    } else if (norm == 2) {
+        g.dnb = e;
+        g.dnw = e * centered_v * rstd;
+        g.d_prenorm = nw * rstd * (e - e * inv_n - rstd * rstd * centered_v * centered_v * e * inv_n);
+    } else if (norm == 3) {
+        g.dnb = e;
+        g.dnw = e * centered_v * rstd;
+        g.d_prenorm = nw * rstd * (e - e * inv_m - rstd * rstd * centered_v * centered_v * e * inv_m);
+    }
+    return g;
+}
+
+// Optimiser hyper-parameters as the update kernels consume them
+// (backward.cu:105-154; bias corrections precomputed per call).
+struct OptParams {
+    uint32_t kind;      // 0 SGD, 1 Adam
+    float beta1, beta2, epsilon;
+    uint32_t nesterov;
+    float bc1, bc2;     // 1 - beta1^step, 1 - beta2^step (Adam)
+};
+
+// backward.cu:105-154, one element.  p, v, m are the fp32 master and moments
+// (in/out); grad_acc is the raw accumulated gradient, already / LOSS_SCALE.
+__device__ __forceinline__ void optimiser_step(float &p, float &v, float &mm, float grad_acc, float inv_m,
+                                               float lr, float clamp, const OptParams &o,
+                                               uint32_t regularisation, float regu_coeff, bool apply_regul) {
+    const float val = grad_acc * inv_m;
+    if (apply_regul) {
+        const float sign = p > 0.0f ? 1.0f : (p < 0.0f ? -1.0f : 0.0f);  // math.cuh:60-66 on master
+        if (regularisation == 1) p -= regu_coeff * sign;
+        if (regularisation == 2) p -= 2.0f * regu_coeff * p;
+    }
+    if (o.kind == 0) {
+        const float dl = o.beta1 * v + val;
+        v = dl;
+        float u = lr * (o.nesterov ? val + o.beta1 * dl : dl);
+        u = fminf(fmaxf(u, -clamp), clamp);
+        p -= u;
+    } else if (o.kind == 1) {
+        const float dml = o.beta1 * mm + (1.0f - o.beta1) * val;
+        const float dvl = o.beta2 * v + (1.0f - o.beta2) * val * val;
+        mm = dml;
+        v = dvl;
+        const float mc = dml / o.bc1;
+        const float vc = dvl / o.bc2;
+        float u = lr * (mc / (sqrtf(vc) + o.epsilon));
+        u = fminf(fmaxf(u, -clamp), clamp);
+        p -= u;
+    }
+}
+
+}  // namespace skl

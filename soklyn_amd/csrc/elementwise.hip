@@ -1,0 +1,371 @@
+// elementwise.hip — bandwidth-bound kernels of the DenseBlock hot path
+// (gfx950, wave64): fill / cast, norm + activation + dropout, softmax, output
+// error, hidden error from a given sum, column reductions + vector optimiser,
+// split-K dW reduction + optimiser.
+#include "launch.h"
+
+namespace skl {
+
+template <typename T> __device__ __forceinline__ T ldv(const void *p, uint64_t i) {
+    return reinterpret_cast<const T *>(p)[i];
+}
+template <typename T> __device__ __forceinline__ void stv(void *p, uint64_t i, T v) {
+    reinterpret_cast<T *>(p)[i] = v;
+}
+
+static inline uint32_t cdiv(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
+
+// ---- fill / cast (math.cuh:69-73, util.cuh:9-19) -------------------------------------
+template <typename T> __global__ void fill_kernel(T *dst, T v, uint64_t n) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+        dst[i] = v;
+}
+
+template <typename S, typename D> __global__ void cast_kernel(const S *src, D *dst, uint64_t n) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+        dst[i] = (D)src[i];
+}
+
+static dim3 grid_for(uint64_t n, uint32_t block) {
+    uint64_t g = (n + block - 1) / block;
+    if (g > 65536) g = 65536;
+    if (g == 0) g = 1;
+    return dim3((uint32_t)g);
+}
+
+hipError_t launch_fill(void *dst, uint32_t dtype, float v, size_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    if (dtype == 1)
+        hipLaunchKernelGGL(fill_kernel<half_t>, grid_for(n, 256), dim3(256), 0, s, (half_t *)dst, (half_t)v,
+                           (uint64_t)n);
+    else
+        hipLaunchKernelGGL(fill_kernel<float>, grid_for(n, 256), dim3(256), 0, s, (float *)dst, v, (uint64_t)n);
+    return hipGetLastError();
+}
+
+hipError_t launch_cast(const void *src, uint32_t sdt, void *dst, uint32_t ddt, size_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    if (sdt == 0 && ddt == 1)
+        hipLaunchKernelGGL((cast_kernel<float, half_t>), grid_for(n, 256), dim3(256), 0, s, (const float *)src,
+                           (half_t *)dst, (uint64_t)n);
+    else if (sdt == 1 && ddt == 0)
+        hipLaunchKernelGGL((cast_kernel<half_t, float>), grid_for(n, 256), dim3(256), 0, s, (const half_t *)src,
+                           (float *)dst, (uint64_t)n);
+    else if (sdt == 0 && ddt == 0)
+        hipLaunchKernelGGL((cast_kernel<float, float>), grid_for(n, 256), dim3(256), 0, s, (const float *)src,
+                           (float *)dst, (uint64_t)n);
+    else
+        hipLaunchKernelGGL((cast_kernel<half_t, half_t>), grid_for(n, 256), dim3(256), 0, s, (const half_t *)src,
+                           (half_t *)dst, (uint64_t)n);
+    return hipGetLastError();
+}
+
+// ---- block reduction (256 threads = 4 waves), fixed order ---------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ float block_sum256(float v, float *red) {
+    v = wave_sum(v);
+    const uint32_t w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63u) == 0) red[w] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+__device__ __forceinline__ float block_max256(float v, float *red) {
+    v = wave_max(v);
+    const uint32_t w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63u) == 0) red[w] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// act + dropout of one element (forward.cu:139-160), input = rounded preact.
+template <typename T>
+__device__ __forceinline__ void act_dropout(const RowNormArgs &a, uint64_t idx, uint32_t row, uint32_t col, T pre) {
+    const float v = activation(a.act, to_f32(pre), a.leaky);
+    stv<T>(a.predrop, idx, from_f32<T>(v));
+    if (a.use_dropout) {
+        if (dropout_u(col, row, a.seed + row * 7u) >= a.p) {
+            const float scale = 1.0f / (1.0f - a.p);
+            stv<T>(a.mask, idx, from_f32<T>(scale));
+            stv<T>(a.out, idx, from_f32<T>(v * scale));
+        } else {
+            stv<T>(a.mask, idx, (T)0);
+            stv<T>(a.out, idx, (T)0);
+        }
+    } else {
+        stv<T>(a.out, idx, from_f32<T>(v));
+    }
+}
+
+// RMSNorm / LayerNorm over one row per workgroup (forward.cu:44-126), then act + dropout.
+template <typename T> __global__ void __launch_bounds__(256) norm_rows_kernel(RowNormArgs a) {
+    __shared__ float red[4];
+    const uint32_t row = blockIdx.x;
+    const uint32_t n = a.n;
+    const uint64_t base = (uint64_t)row * n;
+    if (a.norm == 1) {
+        float sq = 0.0f;
+        for (uint32_t c = threadIdx.x; c < n; c += 256) {
+            const float v = to_f32(ldv<T>(a.prenorm, base + c));
+            sq = fmaf(v, v, sq);
+        }
+        sq = block_sum256(sq, red);
+        const float var = sq / (float)n + 1e-6f;
+        const float rstd32 = 1.0f / sqrtf(var);
+        const T rstd = from_f32<T>(rstd32);
+        if (threadIdx.x == 0) stv<T>(a.norm_rstd, row, rstd);
+        for (uint32_t c = threadIdx.x; c < n; c += 256) {
+            const T z = ldv<T>(a.prenorm, base + c);
+            stv<T>(a.centered, base + c, z);
+            // T arithmetic: (prenorm * rstd) * norm_w, each product rounded to T
+            const T pre = from_f32<T>(to_f32(from_f32<T>(to_f32(z) * to_f32(rstd))) * to_f32(ldv<T>(a.norm_w, c)));
+            stv<T>(a.preact, base + c, pre);
+            act_dropout<T>(a, base + c, row, c, pre);
+        }
+    } else {
+        float s = 0.0f;
+        for (uint32_t c = threadIdx.x; c < n; c += 256) s += to_f32(ldv<T>(a.prenorm, base + c));
+        s = block_sum256(s, red);
+        const float mean = s / (float)n;
+        float ss = 0.0f;
+        for (uint32_t c = threadIdx.x; c < n; c += 256) {
+            const float v = to_f32(ldv<T>(a.prenorm, base + c)) - mean;
+            ss = fmaf(v, v, ss);
+        }
+        ss = block_sum256(ss, red);
+        const float var = ss / (float)n + 1e-6f;
+        const float rstd32 = 1.0f / sqrtf(var);
+        if (threadIdx.x == 0) stv<T>(a.norm_rstd, row, from_f32<T>(rstd32));
+        for (uint32_t c = threadIdx.x; c < n; c += 256) {
+            const float v = to_f32(ldv<T>(a.prenorm, base + c)) - mean;
+            stv<T>(a.centered, base + c, from_f32<T>(v));
+            const T pre = from_f32<T>(
+                fmaf(v * rstd32, to_f32(ldv<T>(a.norm_w, c)), to_f32(ldv<T>(a.norm_b, c))));
+            stv<T>(a.preact, base + c, pre);
+            act_dropout<T>(a, base + c, row, c, pre);
+        }
+    }
+}
+
+// BatchNorm: one thread per column over the batch rows (forward.cu:74-126 with
+// norm == 3), then act + dropout.  Consecutive threads read consecutive columns.
+template <typename T> __global__ void __launch_bounds__(256) norm_cols_kernel(RowNormArgs a) {
+    const uint32_t col = blockIdx.x * 256 + threadIdx.x;
+    if (col >= a.n) return;
+    const uint32_t n = a.n, m = a.m;
+    float s = 0.0f;
+    for (uint32_t r = 0; r < m; ++r) s += to_f32(ldv<T>(a.prenorm, (uint64_t)r * n + col));
+    const float mean = s / (float)m;
+    float ss = 0.0f;
+    for (uint32_t r = 0; r < m; ++r) {
+        const float v = to_f32(ldv<T>(a.prenorm, (uint64_t)r * n + col)) - mean;
+        ss = fmaf(v, v, ss);
+    }
+    const float var = ss / (float)m + 1e-6f;
+    const float rstd32 = 1.0f / sqrtf(var);
+    stv<T>(a.norm_rstd, col, from_f32<T>(rstd32));
+    const float g = to_f32(ldv<T>(a.norm_w, col)), b = to_f32(ldv<T>(a.norm_b, col));
+    for (uint32_t r = 0; r < m; ++r) {
+        const uint64_t idx = (uint64_t)r * n + col;
+        const float v = to_f32(ldv<T>(a.prenorm, idx)) - mean;
+        stv<T>(a.centered, idx, from_f32<T>(v));
+        const T pre = from_f32<T>(fmaf(v * rstd32, g, b));
+        stv<T>(a.preact, idx, pre);
+        act_dropout<T>(a, idx, r, col, pre);
+    }
+}
+
+hipError_t launch_norm_act(const RowNormArgs &a, hipStream_t s) {
+    if (a.m == 0 || a.n == 0) return hipSuccess;
+    if (a.norm == 3) {
+        if (a.dtype == 1)
+            hipLaunchKernelGGL(norm_cols_kernel<half_t>, dim3(cdiv(a.n, 256)), dim3(256), 0, s, a);
+        else
+            hipLaunchKernelGGL(norm_cols_kernel<float>, dim3(cdiv(a.n, 256)), dim3(256), 0, s, a);
+    } else {
+        if (a.dtype == 1)
+            hipLaunchKernelGGL(norm_rows_kernel<half_t>, dim3(a.m), dim3(256), 0, s, a);
+        else
+            hipLaunchKernelGGL(norm_rows_kernel<float>, dim3(a.m), dim3(256), 0, s, a);
+    }
+    return hipGetLastError();
+}
+
+// ---- softmax (util.cu:95-173), one row per workgroup, in place ----------------------
+template <typename T> __global__ void __launch_bounds__(256) softmax_kernel(T *out, uint32_t n) {
+    __shared__ float red[4];
+    const uint64_t base = (uint64_t)blockIdx.x * n;
+    float mx = -INFINITY;
+    for (uint32_t c = threadIdx.x; c < n; c += 256) mx = fmaxf(mx, to_f32(out[base + c]));
+    mx = block_max256(mx, red);
+    float s = 0.0f;
+    for (uint32_t c = threadIdx.x; c < n; c += 256) s += expf(to_f32(out[base + c]) - mx);
+    s = block_sum256(s, red);
+    for (uint32_t c = threadIdx.x; c < n; c += 256) out[base + c] = from_f32<T>(expf(to_f32(out[base + c]) - mx) / s);
+}
+
+hipError_t launch_softmax(uint32_t dtype, void *out, uint32_t rows, uint32_t n, hipStream_t s) {
+    if (rows == 0 || n == 0) return hipSuccess;
+    if (dtype == 1)
+        hipLaunchKernelGGL(softmax_kernel<half_t>, dim3(rows), dim3(256), 0, s, (half_t *)out, n);
+    else
+        hipLaunchKernelGGL(softmax_kernel<float>, dim3(rows), dim3(256), 0, s, (float *)out, n);
+    return hipGetLastError();
+}
+
+// ---- error kernels ------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ void write_err(const ErrArgs &a, uint64_t idx, uint32_t row, uint32_t col, float e) {
+    a.grad[idx] = e;
+    float dp = e;
+    if (a.norm) {
+        const float rstd = to_f32(ldv<T>(a.norm_rstd, a.norm == 3 ? col : row));
+        const float pv = a.norm == 1 ? to_f32(ldv<T>(a.prenorm, idx)) : 0.0f;
+        const float cv = a.norm >= 2 ? to_f32(ldv<T>(a.centered, idx)) : 0.0f;
+        const NormGrad g = norm_grad(a.norm, e, pv, cv, rstd, a.nw[col], a.inv_n, a.inv_m);
+        dp = g.d_prenorm;
+        a.d_norm_w[idx] = g.dnw;
+        a.d_norm_b[idx] = g.dnb;
+    }
+    dp = dp * a.loss_scale;
+    a.d_prenorm[idx] = dp;
+    if (a.d_prenorm_h) a.d_prenorm_h[idx] = (half_t)dp;
+}
+
+// backward.cu:12-56
+template <typename T> __global__ void output_error_kernel(ErrArgs a) {
+    const uint64_t total = (uint64_t)a.rows * a.n;
+    for (uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (uint64_t)gridDim.x * blockDim.x) {
+        const uint32_t row = (uint32_t)(idx / a.n), col = (uint32_t)(idx % a.n);
+        const float o = activation(a.act, to_f32(ldv<T>(a.out, idx)), a.leaky);
+        const float t = to_f32(ldv<T>(a.target, idx));
+        float e = 0.0f;
+        if (a.loss == 0) {
+            e = activation_derivative(a.act, o - t, o, to_f32(ldv<T>(a.preact, idx)), a.leaky);
+        } else if ((a.loss == 1 && a.act == 5) || (a.loss == 2 && a.act == 1)) {
+            e = o - t;
+        }
+        write_err<T>(a, idx, row, col, e);
+    }
+}
+
+// backward.cu:79-100 with s supplied
+template <typename T> __global__ void error_from_sum_kernel(ErrArgs a) {
+    const uint64_t total = (uint64_t)a.rows * a.n;
+    for (uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (uint64_t)gridDim.x * blockDim.x) {
+        const uint32_t row = (uint32_t)(idx / a.n), col = (uint32_t)(idx % a.n);
+        const float d = activation_derivative(a.act, a.s[idx], to_f32(ldv<T>(a.predrop, idx)),
+                                              to_f32(ldv<T>(a.preact, idx)), a.leaky);
+        write_err<T>(a, idx, row, col, to_f32(ldv<T>(a.mask, idx)) * d);
+    }
+}
+
+hipError_t launch_output_error(const ErrArgs &a, hipStream_t s) {
+    const uint64_t total = (uint64_t)a.rows * a.n;
+    if (total == 0) return hipSuccess;
+    if (a.dtype == 1)
+        hipLaunchKernelGGL(output_error_kernel<half_t>, grid_for(total, 256), dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL(output_error_kernel<float>, grid_for(total, 256), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_error_from_sum(const ErrArgs &a, hipStream_t s) {
+    const uint64_t total = (uint64_t)a.rows * a.n;
+    if (total == 0) return hipSuccess;
+    if (a.dtype == 1)
+        hipLaunchKernelGGL(error_from_sum_kernel<half_t>, grid_for(total, 256), dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL(error_from_sum_kernel<float>, grid_for(total, 256), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+// ---- column sums (backward.cu:187-194) + vector optimiser (backward.cu:198-225) -------
+__global__ void __launch_bounds__(256) colsum_kernel(VecOptArgs a) {
+    const uint32_t col = blockIdx.x * 256 + threadIdx.x;
+    if (col >= a.n) return;
+    const uint32_t per = (a.rows + a.splits - 1) / a.splits;
+    const uint32_t r0 = blockIdx.y * per;
+    const uint32_t r1 = min(a.rows, r0 + per);
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        if (!a.src[k]) continue;
+        float s = 0.0f;
+        for (uint32_t r = r0; r < r1; ++r) s += a.src[k][(uint64_t)r * a.n + col];
+        a.partials[((uint64_t)blockIdx.y * 3 + k) * a.n + col] = s;
+    }
+}
+
+template <typename T> __global__ void __launch_bounds__(256) vec_opt_kernel(VecOptArgs a) {
+    const uint32_t col = blockIdx.x * 256 + threadIdx.x;
+    if (col >= a.n) return;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        if (!a.enabled[k]) continue;
+        float s = 0.0f;
+        for (uint32_t sp = 0; sp < a.splits; ++sp) s += a.partials[((uint64_t)sp * 3 + k) * a.n + col];
+        float p = a.master[k][col], v = a.dv[k][col], mm = a.dm[k][col];
+        optimiser_step(p, v, mm, s * kLossScaleInv, a.inv_m, a.lr, a.clamp, a.opt[k], 0, 0.0f, false);
+        a.master[k][col] = p;
+        a.dv[k][col] = v;
+        a.dm[k][col] = mm;
+        if (a.param[k]) stv<T>(a.param[k], col, from_f32<T>(p));
+    }
+}
+
+hipError_t launch_colsum(const VecOptArgs &a, hipStream_t s) {
+    if (a.n == 0) return hipSuccess;
+    hipLaunchKernelGGL(colsum_kernel, dim3(cdiv(a.n, 256), a.splits), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_vec_opt(const VecOptArgs &a, hipStream_t s) {
+    if (a.n == 0) return hipSuccess;
+    if (a.dtype == 1)
+        hipLaunchKernelGGL(vec_opt_kernel<half_t>, dim3(cdiv(a.n, 256)), dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL(vec_opt_kernel<float>, dim3(cdiv(a.n, 256)), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+// ---- split-K dW reduction + W optimiser ----------------------------------------------
+template <typename T> __global__ void dw_reduce_opt_kernel(DwReduceArgs a) {
+    const uint64_t total = (uint64_t)a.rows * a.n;
+    for (uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (uint64_t)gridDim.x * blockDim.x) {
+        float s = 0.0f;
+        for (uint32_t sp = 0; sp < a.splits; ++sp) s += a.partials[(uint64_t)sp * total + idx];
+        const OptEpi &e = a.e;
+        float p = e.master[idx], v = e.dv[idx], mm = e.dm[idx];
+        optimiser_step(p, v, mm, s * kLossScaleInv, e.inv_m, e.lr, e.clamp, e.opt, e.regularisation, e.regu_coeff,
+                       true);
+        e.master[idx] = p;
+        e.dv[idx] = v;
+        e.dm[idx] = mm;
+        if (e.param) stv<T>(e.param, idx, from_f32<T>(p));
+    }
+}
+
+hipError_t launch_dw_reduce_opt(const DwReduceArgs &a, hipStream_t s) {
+    const uint64_t total = (uint64_t)a.rows * a.n;
+    if (total == 0) return hipSuccess;
+    if (a.dtype == 1)
+        hipLaunchKernelGGL(dw_reduce_opt_kernel<half_t>, grid_for(total, 256), dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL(dw_reduce_opt_kernel<float>, grid_for(total, 256), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+}  // namespace skl

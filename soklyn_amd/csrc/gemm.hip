@@ -1,0 +1,238 @@
+// gemm.hip — GEMM epilogues and launchers for the three DenseBlock
+// contractions (forward, dX, dW) on gfx950.
+#include "gemm.h"
+#include "launch.h"
+
+namespace skl {
+
+template <typename T> __device__ __forceinline__ T ld_t(const void *p, uint64_t i) {
+    return reinterpret_cast<const T *>(p)[i];
+}
+template <typename T> __device__ __forceinline__ void st_t(void *p, uint64_t i, T v) {
+    reinterpret_cast<T *>(p)[i] = v;
+}
+
+// ---- forward: bias (+ act + dropout) ------------------------------------------
+template <typename T> struct EpiFwdK {
+    typedef FwdEpi Params;
+    __device__ __forceinline__ static void apply(const FwdEpi &e, const GemmShape &sh, uint32_t m, uint32_t n,
+                                                 floatx4 v, uint32_t) {
+        if (m >= sh.M) return;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t c = n + j;
+            if (c >= sh.N) break;
+            float z = v[j];
+            if (e.bias) z = z + to_f32(ld_t<T>(e.bias, c));   // f32 acc + f32(b), one rounding
+            const T zt = from_f32<T>(z);
+            const uint64_t idx = (uint64_t)m * e.ldc + c;
+            st_t<T>(e.z_out, idx, zt);
+            if (e.fuse_act) {
+                const float a = activation(e.act, to_f32(zt), e.leaky);
+                st_t<T>(e.predrop, idx, from_f32<T>(a));
+                if (e.use_dropout) {
+                    if (dropout_u(c, m, e.seed + m * 7u) >= e.p) {
+                        const float scale = 1.0f / (1.0f - e.p);
+                        st_t<T>(e.mask, idx, from_f32<T>(scale));
+                        st_t<T>(e.out, idx, from_f32<T>(a * scale));
+                    } else {
+                        st_t<T>(e.mask, idx, (T)0);
+                        st_t<T>(e.out, idx, (T)0);
+                    }
+                } else {
+                    st_t<T>(e.out, idx, from_f32<T>(a));
+                }
+            }
+        }
+    }
+};
+
+// ---- hidden error: act' * mask, element-local norm gradient --------------------
+template <typename T> struct EpiHiddenK {
+    typedef HiddenEpi Params;
+    __device__ __forceinline__ static void apply(const HiddenEpi &e, const GemmShape &sh, uint32_t m,
+                                                 uint32_t n, floatx4 v, uint32_t) {
+        if (m >= sh.M) return;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t c = n + j;
+            if (c >= sh.N) break;
+            const uint64_t idx = (uint64_t)m * e.ldc + c;
+            const float d = activation_derivative(e.act, v[j], to_f32(ld_t<T>(e.predrop, idx)),
+                                                  to_f32(ld_t<T>(e.preact, idx)), e.leaky);
+            const float err = to_f32(ld_t<T>(e.mask, idx)) * d;
+            e.grad[idx] = err;
+            float dp = err;
+            if (e.norm) {
+                const float rstd = to_f32(ld_t<T>(e.norm_rstd, e.norm == 3 ? c : m));
+                const float pv = e.norm == 1 ? to_f32(ld_t<T>(e.prenorm, idx)) : 0.0f;
+                const float cv = e.norm >= 2 ? to_f32(ld_t<T>(e.centered, idx)) : 0.0f;
+                const NormGrad g = norm_grad(e.norm, err, pv, cv, rstd, e.nw[c], e.inv_n, e.inv_m);
+                dp = g.d_prenorm;
+                e.d_norm_w[idx] = g.dnw;
+                e.d_norm_b[idx] = g.dnb;
+            }
+            dp = dp * e.loss_scale;
+            e.d_prenorm[idx] = dp;
+            if (e.d_prenorm_h) e.d_prenorm_h[idx] = (half_t)dp;
+        }
+    }
+};
+
+// ---- plain fp32 store (input gradient; split-K partials) -----------------------
+struct EpiStoreK {
+    typedef StoreEpi Params;
+    __device__ __forceinline__ static void apply(const StoreEpi &e, const GemmShape &sh, uint32_t m, uint32_t n,
+                                                 floatx4 v, uint32_t split) {
+        if (m >= sh.M) return;
+        float *o = e.out + (uint64_t)split * e.split_stride + (uint64_t)m * e.ldc;
+        if (n + 3 < sh.N && (e.ldc & 3u) == 0) {
+            *reinterpret_cast<floatx4 *>(o + n) = v;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (n + j < sh.N) o[n + j] = v[j];
+        }
+    }
+};
+
+// ---- dW + optimiser on W (fused) -----------------------------------------------
+template <typename T> struct EpiOptK {
+    typedef OptEpi Params;
+    __device__ __forceinline__ static void apply(const OptEpi &e, const GemmShape &sh, uint32_t m, uint32_t n,
+                                                 floatx4 v, uint32_t) {
+        if (m >= sh.M) return;
+        const uint64_t base = (uint64_t)m * e.ldc;
+        if (n + 3 < sh.N && (e.ldc & 3u) == 0) {
+            floatx4 p = *reinterpret_cast<const floatx4 *>(e.master + base + n);
+            floatx4 dv = *reinterpret_cast<const floatx4 *>(e.dv + base + n);
+            floatx4 dm = *reinterpret_cast<const floatx4 *>(e.dm + base + n);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float pj = p[j], vj = dv[j], mj = dm[j];
+                optimiser_step(pj, vj, mj, v[j] * kLossScaleInv, e.inv_m, e.lr, e.clamp, e.opt, e.regularisation,
+                               e.regu_coeff, true);
+                p[j] = pj; dv[j] = vj; dm[j] = mj;
+            }
+            *reinterpret_cast<floatx4 *>(e.master + base + n) = p;
+            *reinterpret_cast<floatx4 *>(e.dv + base + n) = dv;
+            *reinterpret_cast<floatx4 *>(e.dm + base + n) = dm;
+            if (e.param) {
+                T t[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) t[j] = from_f32<T>(p[j]);
+                if constexpr (sizeof(T) == 2) {
+                    *reinterpret_cast<uint64_t *>(reinterpret_cast<T *>(e.param) + base + n) =
+                        __builtin_bit_cast(uint64_t, t);
+                } else {
+                    *reinterpret_cast<floatx4 *>(reinterpret_cast<T *>(e.param) + base + n) =
+                        __builtin_bit_cast(floatx4, t);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t c = n + j;
+                if (c >= sh.N) break;
+                const uint64_t idx = base + c;
+                float pj = e.master[idx], vj = e.dv[idx], mj = e.dm[idx];
+                optimiser_step(pj, vj, mj, v[j] * kLossScaleInv, e.inv_m, e.lr, e.clamp, e.opt, e.regularisation,
+                               e.regu_coeff, true);
+                e.master[idx] = pj;
+                e.dv[idx] = vj;
+                e.dm[idx] = mj;
+                if (e.param) st_t<T>(e.param, idx, from_f32<T>(pj));
+            }
+        }
+    }
+};
+
+// ---- tile configurations ----------------------------------------------------------
+template <typename T, int BM, int BN, int BK, int WM, int WN> struct Cfg {
+    typedef T type;
+    static constexpr int bm = BM, bn = BN, bk = BK, wm = WM, wn = WN, nt = WM * WN * 64;
+};
+typedef Cfg<half_t, 256, 256, 64, 2, 2> CfgH256;
+typedef Cfg<half_t, 128, 128, 64, 2, 2> CfgH128;
+typedef Cfg<float, 128, 128, 32, 2, 2> CfgF128;
+typedef Cfg<float, 64, 64, 32, 2, 2> CfgF64;
+
+template <class C, bool AK, bool BK_, bool VOK, class Epi>
+static hipError_t run(const GemmLaunch &g, const typename Epi::Params &p, hipStream_t s) {
+    typedef typename C::type T;
+    GemmShape sh;
+    sh.M = g.M;
+    sh.N = g.N;
+    sh.K = g.K;
+    sh.lda = g.lda;
+    sh.ldb = g.ldb;
+    sh.tiles_m = (g.M + C::bm - 1) / C::bm;
+    sh.tiles_n = (g.N + C::bn - 1) / C::bn;
+    const uint32_t splits = g.splits ? g.splits : 1;
+    const uint32_t kps_raw = (g.K + splits - 1) / splits;
+    sh.k_per_split = ((kps_raw + C::bk - 1) / C::bk) * C::bk;
+    dim3 grid(sh.tiles_m * sh.tiles_n, 1, splits);
+    hipLaunchKernelGGL((gemm_kernel<T, C::bm, C::bn, C::bk, C::wm, C::wn, AK, BK_, VOK, Epi>), grid,
+                       dim3(C::nt), 0, s, sh, reinterpret_cast<const T *>(g.A),
+                       reinterpret_cast<const T *>(g.B), p);
+    return hipGetLastError();
+}
+
+static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Decide whether both operands can be staged in 16-byte chunks.
+static bool vec_ok(const GemmLaunch &g, int vec) {
+    // contiguous extent of A: K if k-contig else M; of B: K if k-contig else N
+    const uint32_t a_ext = g.a_kcontig ? g.K : g.M;
+    const uint32_t b_ext = g.b_kcontig ? g.K : g.N;
+    return (g.lda % vec) == 0 && (g.ldb % vec) == 0 && (a_ext % vec) == 0 && (b_ext % vec) == 0 &&
+           aligned16(g.A) && aligned16(g.B);
+}
+
+template <class C, bool AK, bool BK_, class Epi>
+static hipError_t dispatch_vec(const GemmLaunch &g, const typename Epi::Params &p, hipStream_t s) {
+    constexpr int VEC = Mfma<typename C::type>::VEC;
+    if (g.a_kcontig != AK || g.b_kcontig != BK_) return hipErrorInvalidValue;
+    return vec_ok(g, VEC) ? run<C, AK, BK_, true, Epi>(g, p, s) : run<C, AK, BK_, false, Epi>(g, p, s);
+}
+
+// Only the (layout, epilogue) pairs the DenseBlock path uses are instantiated:
+//   forward  : A k-contig, B n-contig
+//   dX       : A k-contig, B k-contig
+//   dW       : A m-contig, B n-contig
+template <class C> static hipError_t dispatch_op(const GemmLaunch &g, hipStream_t s) {
+    typedef typename C::type T;
+    switch (g.op) {
+    case Op::Fwd: return dispatch_vec<C, true, false, EpiFwdK<T>>(g, g.fwd, s);
+    case Op::Hidden: return dispatch_vec<C, true, true, EpiHiddenK<T>>(g, g.hid, s);
+    case Op::InputGrad: return dispatch_vec<C, true, true, EpiStoreK>(g, g.st, s);
+    case Op::DwPartial: return dispatch_vec<C, false, false, EpiStoreK>(g, g.st, s);
+    case Op::DwOpt: return dispatch_vec<C, false, false, EpiOptK<T>>(g, g.opt, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+uint32_t gemm_tiles(uint32_t dtype, uint32_t M, uint32_t N) {
+    if (dtype == 1) {
+        const uint32_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
+        if (t256 >= 192) return t256;
+        return ((M + 127) / 128) * ((N + 127) / 128);
+    }
+    const uint32_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
+    if (t128 >= 192) return t128;
+    return ((M + 63) / 64) * ((N + 63) / 64);
+}
+
+uint32_t gemm_bk(uint32_t dtype) { return dtype == 1 ? 64 : 32; }
+
+hipError_t launch_gemm(const GemmLaunch &g, hipStream_t s) {
+    if (g.M == 0 || g.N == 0) return hipSuccess;
+    if (g.dtype == 1) {
+        const uint32_t t256 = ((g.M + 255) / 256) * ((g.N + 255) / 256);
+        return t256 >= 192 ? dispatch_op<CfgH256>(g, s) : dispatch_op<CfgH128>(g, s);
+    }
+    const uint32_t t128 = ((g.M + 127) / 128) * ((g.N + 127) / 128);
+    return t128 >= 192 ? dispatch_op<CfgF128>(g, s) : dispatch_op<CfgF64>(g, s);
+}
+
+}  // namespace skl

@@ -1,0 +1,128 @@
+// launch.h — host-side launchers of the DenseBlock kernels (internal to
+// libsoklyn_hip.so; the public surface is include/soklyn_hip.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "device_math.h"
+
+namespace skl {
+
+// ---- GEMM epilogue parameters ------------------------------------------------
+// Forward: Z = X.W (+b); when fuse_act, act + dropout write predrop/out/mask
+// (forward.cu:8-28 + 130-161 fused; norm Disabled), otherwise Z is the
+// prenorm cache and the row-norm kernel finishes the layer.
+struct FwdEpi {
+    const void *bias;          // T[N] or null
+    void *z_out;               // T [M x ldc]: preact (fused) or prenorm
+    void *predrop, *out, *mask;
+    uint32_t fuse_act, act, use_dropout, seed;
+    float leaky, p;
+    uint32_t ldc, pad;
+};
+
+// Hidden error (backward.cu:79-100 / backward_wmma.cu:304-331).
+struct HiddenEpi {
+    const void *predrop, *preact, *mask, *norm_rstd, *centered, *prenorm;   // T
+    const float *nw;                                                        // master norm_w
+    float *grad, *d_prenorm, *d_norm_w, *d_norm_b;
+    half_t *d_prenorm_h;
+    uint32_t norm, act;
+    float leaky, inv_n, inv_m, loss_scale;
+    uint32_t ldc, pad;
+};
+
+// dW + optimiser on W (backward.cu:180-186 + 227-233).
+struct OptEpi {
+    float *master;        // fp32 master (the parameter itself for fp32 blocks)
+    void *param;          // T copy (null when param is the master)
+    float *dv, *dm;
+    OptParams opt;
+    float lr, clamp, inv_m, regu_coeff;
+    uint32_t regularisation, ldc;
+};
+
+// Plain fp32 store (input gradient) or split-K partial store.
+struct StoreEpi {
+    float *out;
+    uint64_t split_stride;   // elements between split-K partial planes
+    uint32_t ldc, pad;
+};
+
+enum class Op { Fwd, Hidden, InputGrad, DwOpt, DwPartial };
+
+// One GEMM launch.  dtype selects fp16 (MFMA 32x32x16 f16) or fp32
+// (MFMA 32x32x2 f32).  a_kcontig / b_kcontig as in gemm.h.
+struct GemmLaunch {
+    uint32_t dtype;
+    uint32_t M, N, K, lda, ldb;
+    bool a_kcontig, b_kcontig;
+    const void *A, *B;
+    uint32_t splits;      // split-K factor (DwPartial only; 1 otherwise)
+    Op op;
+    FwdEpi fwd;
+    HiddenEpi hid;
+    OptEpi opt;
+    StoreEpi st;
+};
+
+hipError_t launch_gemm(const GemmLaunch &g, hipStream_t stream);
+// Number of output tiles the launcher would use (for split-K sizing).
+uint32_t gemm_tiles(uint32_t dtype, uint32_t M, uint32_t N);
+uint32_t gemm_bk(uint32_t dtype);
+
+// ---- element-wise / row / column kernels -------------------------------------
+hipError_t launch_fill(void *dst, uint32_t dtype, float v, size_t n, hipStream_t s);
+hipError_t launch_cast(const void *src, uint32_t sdt, void *dst, uint32_t ddt, size_t n, hipStream_t s);
+
+struct RowNormArgs {
+    uint32_t dtype, m, n, norm, act, use_dropout, seed;
+    float leaky, p;
+    const void *prenorm, *norm_w, *norm_b;
+    void *centered, *preact, *predrop, *out, *mask, *norm_rstd;
+};
+// fwd1 + fwd2 fused (RMS / LN per row; BN per column then act).
+hipError_t launch_norm_act(const RowNormArgs &a, hipStream_t s);
+
+hipError_t launch_softmax(uint32_t dtype, void *out, uint32_t rows, uint32_t n, hipStream_t s);
+
+struct ErrArgs {
+    uint32_t dtype, rows, n, norm, act, loss;
+    float leaky, inv_n, inv_m, loss_scale;
+    const void *out, *preact, *target;                 // output error
+    const float *s;                                    // error_from_sum
+    const void *predrop, *mask;                        // error_from_sum
+    const void *norm_rstd, *centered, *prenorm;
+    const float *nw;
+    float *grad, *d_prenorm, *d_norm_w, *d_norm_b;
+    half_t *d_prenorm_h;
+};
+hipError_t launch_output_error(const ErrArgs &a, hipStream_t s);
+hipError_t launch_error_from_sum(const ErrArgs &a, hipStream_t s);
+
+// Column sums of up to three fp32 [rows x n] arrays into partials
+// [splits x 3 x n]; then the bias / norm-parameter optimiser.
+struct VecOptArgs {
+    uint32_t dtype, rows, n, splits;
+    const float *src[3];          // d_prenorm (bias), d_norm_w, d_norm_b (null = skip)
+    float *partials;              // [splits][3][n]
+    // targets: 0 bias, 1 norm_w, 2 norm_b
+    void *param[3];
+    float *master[3], *dv[3], *dm[3];
+    uint32_t enabled[3];
+    OptParams opt[3];
+    float lr, clamp, inv_m;
+};
+hipError_t launch_colsum(const VecOptArgs &a, hipStream_t s);
+hipError_t launch_vec_opt(const VecOptArgs &a, hipStream_t s);
+
+// Split-K dW reduction + W optimiser.
+struct DwReduceArgs {
+    uint32_t dtype, rows, n, splits;
+    const float *partials;         // [splits][rows * n]
+    OptEpi e;
+};
+hipError_t launch_dw_reduce_opt(const DwReduceArgs &a, hipStream_t s);
+
+}  // namespace skl

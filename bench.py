@@ -80,7 +80,8 @@ def main():
     M, K, N, half = cfg["M"], cfg["K"], cfg["N"], cfg["half"]
     dt = torch.float16 if half else torch.float32
     torch.manual_seed(0)
-    stream = torch.cuda.current_stream()
+    stream = torch.cuda.Stream()          # explicit, default priority (stream 0 has handle 0)
+    torch.cuda.set_stream(stream)
     ctx = abi.Context(0, 16)
     ctx.set_stream(stream.cuda_stream)
     ctx.set_sync(False)

@@ -177,7 +177,8 @@ int32_t skl_ctx_create(int32_t ordinal, uint32_t tile_dim, skl_ctx **out) {
     c->sync = 1;
     c->ws = nullptr;
     c->ws_bytes = 0;
-    hipError_t e = hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking);
+    // blocking w.r.t. the legacy null stream, so callers on stream 0 stay ordered
+    hipError_t e = hipStreamCreateWithFlags(&c->own_stream, hipStreamDefault);
     if (e != hipSuccess) {
         delete c;
         return hip_status(e);

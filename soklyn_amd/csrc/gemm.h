@@ -66,11 +66,15 @@ template <> struct Mfma<half_t> {
 template <> struct Mfma<float> {
     static constexpr int VEC = 4;
     static constexpr int KSTEP = 8;     // 4 MFMAs of k=2, lane-half h holds k = 4h + s
+    // The four k-slices are spelled out with constant lanes: an unrolled
+    // `bop[s]` loop here was compiled to four MFMAs on lane 0 only.
     __device__ __forceinline__ static void run(floatx16 &acc, const u32x4 &bop, const u32x4 &aop) {
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__builtin_bit_cast(float, bop[s]),
-                                                       __builtin_bit_cast(float, aop[s]), acc, 0, 0, 0);
+        const floatx4 b = __builtin_bit_cast(floatx4, bop);
+        const floatx4 a = __builtin_bit_cast(floatx4, aop);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(b.x, a.x, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(b.y, a.y, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(b.z, a.z, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(b.w, a.w, acc, 0, 0, 0);
     }
 };
 

@@ -1,5 +1,7 @@
 // gemm.hip — GEMM epilogues and launchers for the three DenseBlock
 // contractions (forward, dX, dW) on gfx950.
+#include <stdlib.h>
+
 #include "gemm.h"
 #include "launch.h"
 
@@ -152,7 +154,8 @@ template <typename T, int BM, int BN, int BK, int WM, int WN> struct Cfg {
     typedef T type;
     static constexpr int bm = BM, bn = BN, bk = BK, wm = WM, wn = WN, nt = WM * WN * 64;
 };
-typedef Cfg<half_t, 256, 256, 64, 2, 2> CfgH256;
+typedef Cfg<half_t, 256, 256, 64, 2, 2> CfgH256;     // 4 waves, 128x128 per wave, 1 wave / SIMD
+typedef Cfg<half_t, 256, 256, 64, 2, 4> CfgH256w8;   // 8 waves, 128x64 per wave, 2 waves / SIMD
 typedef Cfg<half_t, 128, 128, 64, 2, 2> CfgH128;
 typedef Cfg<float, 128, 128, 32, 2, 2> CfgF128;
 typedef Cfg<float, 64, 64, 32, 2, 2> CfgF64;
@@ -225,11 +228,21 @@ uint32_t gemm_tiles(uint32_t dtype, uint32_t M, uint32_t N) {
 
 uint32_t gemm_bk(uint32_t dtype) { return dtype == 1 ? 64 : 32; }
 
+// Large fp16 tile variant: SOKLYN_GEMM_WAVES=4|8 (tuning override; default 8).
+static int large_tile_waves() {
+    static int w = [] {
+        const char *e = getenv("SOKLYN_GEMM_WAVES");
+        return (e && atoi(e) == 4) ? 4 : 8;
+    }();
+    return w;
+}
+
 hipError_t launch_gemm(const GemmLaunch &g, hipStream_t s) {
     if (g.M == 0 || g.N == 0) return hipSuccess;
     if (g.dtype == 1) {
         const uint32_t t256 = ((g.M + 255) / 256) * ((g.N + 255) / 256);
-        return t256 >= 192 ? dispatch_op<CfgH256>(g, s) : dispatch_op<CfgH128>(g, s);
+        if (t256 < 192) return dispatch_op<CfgH128>(g, s);
+        return large_tile_waves() == 4 ? dispatch_op<CfgH256>(g, s) : dispatch_op<CfgH256w8>(g, s);
     }
     const uint32_t t128 = ((g.M + 127) / 128) * ((g.N + 127) / 128);
     return t128 >= 192 ? dispatch_op<CfgF128>(g, s) : dispatch_op<CfgF64>(g, s);

@@ -16,8 +16,12 @@ def pytest_configure(config):
 def ctx():
     import torch
     from soklyn_amd import abi
+    # An explicit (default-priority) stream: torch's legacy default stream has handle 0,
+    # which the C ABI would read as "use the context's own stream".
+    s = torch.cuda.Stream()
+    torch.cuda.set_stream(s)
     c = abi.Context(0, 16)
-    c.set_stream(torch.cuda.current_stream().cuda_stream)
+    c.set_stream(s.cuda_stream)
     yield c
     torch.cuda.synchronize()
     c.close()

@@ -66,6 +66,17 @@ int32_t ensure_ws(skl_ctx *ctx, size_t bytes) {
 
 size_t elem_size(uint32_t dtype) { return dtype == SKL_F16 ? 2 : 4; }
 
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Large fp16 GEMMs whose operands are not k-contiguous run on transposed
+// copies (workspace) instead: one HBM pass per operand buys the faster
+// k-contiguous MFMA staging.  Shapes must allow 16-byte chunks everywhere.
+bool use_transposed_operands(uint32_t dtype, uint32_t M, uint32_t N, uint32_t K, uint32_t ld) {
+    if (dtype != SKL_F16) return false;
+    if ((M | N | K | ld) & 7u) return false;
+    return gemm_tiles(dtype, M, N) >= 192 && ((M + 255) / 256) * ((N + 255) / 256) >= 192;
+}
+
 // Common configuration checks of a block descriptor.
 int32_t check_desc(const skl_ctx *ctx, const skl_dense_desc *b) {
     SKL_CHECK(b, SKL_ERR_NULL_POINTER);
@@ -319,6 +330,15 @@ int32_t skl_dense_forward(skl_ctx *ctx, const skl_dense_desc *b, const void *in,
     g.fwd.leaky = b->act == SKL_ACT_LEAKY_RELU ? b->leaky : 0.0f;       // ffn_device.rs:32-35
     g.fwd.p = b->mask_coeff;
     g.fwd.ldc = b->outputs;
+    if (use_transposed_operands(b->dtype, batch, b->outputs, b->inputs, in_cols) && aligned16(in)) {
+        // W^T [N x K] once per call, then the k-contiguous GEMM layout
+        const size_t wt_bytes = (size_t)b->inputs * b->outputs * sizeof(uint16_t);
+        if ((r = ensure_ws(ctx, wt_bytes))) return r;
+        SKL_TRY(launch_transpose_h(b->w, ctx->ws, b->inputs, b->outputs, b->outputs, b->inputs, ctx->stream));
+        g.B = ctx->ws;
+        g.ldb = b->inputs;
+        g.b_kcontig = true;
+    }
     SKL_TRY(launch_gemm(g, ctx->stream));
 
     if (b->norm != SKL_NORM_DISABLED) {
@@ -520,18 +540,20 @@ static int32_t backward_impl(skl_ctx *ctx, const skl_dense_desc *b, const void *
     }
 
     // column partial sums for db / dNorm sums share the workspace
-    const uint32_t col_blocks = (N + 255) / 256;
-    uint32_t csplits = (1024 + col_blocks - 1) / col_blocks;
-    const uint32_t cmax = batch / 32 > 0 ? batch / 32 : 1;
-    if (csplits > cmax) csplits = cmax;
-    if (csplits > 256) csplits = 256;
-    if (csplits < 1) csplits = 1;
+    const uint32_t csplits = colsum_splits(batch, N);
 
+    const bool transposed = splits == 1 && use_transposed_operands(b->dtype, K, N, batch, in_cols) &&
+                            aligned16(in) && aligned16(b->d_prenorm_h);
     const size_t dw_bytes = splits > 1 ? (size_t)splits * K * N * sizeof(float) : 0;
     const size_t col_bytes = (size_t)csplits * 3 * N * sizeof(float);
-    if ((r = ensure_ws(ctx, dw_bytes + col_bytes))) return r;
-    float *ws_dw = reinterpret_cast<float *>(ctx->ws);
-    float *ws_col = reinterpret_cast<float *>(reinterpret_cast<char *>(ctx->ws) + dw_bytes);
+    const size_t xt_bytes = transposed ? (size_t)K * batch * sizeof(uint16_t) : 0;
+    const size_t pt_bytes = transposed ? (size_t)N * batch * sizeof(uint16_t) : 0;
+    if ((r = ensure_ws(ctx, dw_bytes + col_bytes + xt_bytes + pt_bytes))) return r;
+    char *ws = reinterpret_cast<char *>(ctx->ws);
+    float *ws_dw = reinterpret_cast<float *>(ws);
+    float *ws_col = reinterpret_cast<float *>(ws + dw_bytes);
+    void *ws_xt = ws + dw_bytes + col_bytes;
+    void *ws_pt = ws + dw_bytes + col_bytes + xt_bytes;
 
     GemmLaunch g{};
     g.dtype = b->dtype;
@@ -545,6 +567,17 @@ static int32_t backward_impl(skl_ctx *ctx, const skl_dense_desc *b, const void *
     g.A = in;
     g.B = f16 ? b->d_prenorm_h : b->d_prenorm;
     g.splits = splits;
+    if (transposed) {
+        // X^T [K x batch] and dP^T [N x batch]: both operands k-contiguous
+        SKL_TRY(launch_transpose_h(in, ws_xt, batch, K, in_cols, batch, ctx->stream));
+        SKL_TRY(launch_transpose_h(b->d_prenorm_h, ws_pt, batch, N, N, batch, ctx->stream));
+        g.A = ws_xt;
+        g.B = ws_pt;
+        g.lda = batch;
+        g.ldb = batch;
+        g.a_kcontig = true;
+        g.b_kcontig = true;
+    }
     if (splits == 1) {
         g.op = Op::DwOpt;
         g.opt = oe;

@@ -18,17 +18,53 @@ __device__ __forceinline__ float to_f32(float v) { return v; }
 __device__ __forceinline__ float to_f32(half_t v) { return (float)v; }
 template <typename T> __device__ __forceinline__ T from_f32(float v) { return (T)v; }  // RNE
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+// 4 consecutive T elements <-> 4 floats (8-byte loads for fp16, 16-byte for fp32).
+// The element index i must be a multiple of 4 and the base 16-byte aligned.
+template <typename T> __device__ __forceinline__ f32x4 load4(const void *p, uint64_t i) {
+    if constexpr (sizeof(T) == 2) {
+        const f16x4 h = *reinterpret_cast<const f16x4 *>(reinterpret_cast<const half_t *>(p) + i);
+        return f32x4{(float)h.x, (float)h.y, (float)h.z, (float)h.w};
+    } else {
+        return *reinterpret_cast<const f32x4 *>(reinterpret_cast<const float *>(p) + i);
+    }
+}
+template <typename T> __device__ __forceinline__ void store4(void *p, uint64_t i, f32x4 v) {
+    if constexpr (sizeof(T) == 2) {
+        *reinterpret_cast<f16x4 *>(reinterpret_cast<half_t *>(p) + i) =
+            f16x4{(half_t)v.x, (half_t)v.y, (half_t)v.z, (half_t)v.w};
+    } else {
+        *reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(p) + i) = v;
+    }
+}
+// Round 4 floats through T (the value a T store followed by a load would give).
+template <typename T> __device__ __forceinline__ f32x4 round4(f32x4 v) {
+    if constexpr (sizeof(T) == 2) {
+        return f32x4{(float)(half_t)v.x, (float)(half_t)v.y, (float)(half_t)v.z, (float)(half_t)v.w};
+    } else {
+        return v;
+    }
+}
+
 constexpr float kLossScale = 512.0f;            // backward.cu:8
 constexpr float kLossScaleInv = 1.0f / 512.0f;  // backward.cu:9
+
+// 1 / (1 + e^-x) from the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32):
+// a few ulp, well inside every tolerance of this path; saturates to 0 / 1.
+__device__ __forceinline__ float sigmoid_fast(float x) {
+    return __builtin_amdgcn_rcpf(1.0f + __expf(-x));
+}
 
 // util.cu:8-47
 __device__ __forceinline__ float activation(uint32_t act, float x, float leaky) {
     switch (act) {
-    case 1: return 1.0f / (1.0f + expf(-x));
+    case 1: return sigmoid_fast(x);
     case 2: return fmaxf(0.0f, x);
     case 3: return x > 0.0f ? x : leaky * x;
     case 4: return tanhf(x);
-    case 6: return x / (1.0f + expf(-x));
+    case 6: return x * sigmoid_fast(x);
     case 7: {
         const float e_x = expf(x);
         const float sp = x > 20.0f ? x : logf(1.0f + e_x);   // softplus with the reference cutoff
@@ -49,7 +85,7 @@ __device__ __forceinline__ float activation_derivative(uint32_t act, float err, 
     case 3: return err * (out_v > 0.0f ? 1.0f : leaky);
     case 4: return err * (1.0f - out_v * out_v);
     case 6: {
-        const float sig = 1.0f / (1.0f + expf(-in_x));
+        const float sig = sigmoid_fast(in_x);
         return err * (sig + out_v * (1.0f - sig));
     }
     case 7: {

@@ -15,6 +15,8 @@ template <typename T> __device__ __forceinline__ void stv(void *p, uint64_t i, T
 
 static inline uint32_t cdiv(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
 
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
 // ---- fill / cast (math.cuh:69-73, util.cuh:9-19) -------------------------------------
 template <typename T> __global__ void fill_kernel(T *dst, T v, uint64_t n) {
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
@@ -272,23 +274,111 @@ template <typename T> __global__ void error_from_sum_kernel(ErrArgs a) {
     }
 }
 
+// Vector forms: each thread owns 4 consecutive elements of one row (n % 4 == 0,
+// 16-byte aligned buffers): 16-byte fp32 / 8-byte fp16 accesses, 32-bit indexing.
+template <typename T>
+__device__ __forceinline__ void write_err4(const ErrArgs &a, uint64_t idx, uint32_t row, uint32_t col, f32x4 e) {
+    *reinterpret_cast<f32x4 *>(a.grad + idx) = e;
+    f32x4 dp = e;
+    if (a.norm) {
+        const f32x4 pv = a.norm == 1 ? load4<T>(a.prenorm, idx) : f32x4{0, 0, 0, 0};
+        const f32x4 cv = a.norm >= 2 ? load4<T>(a.centered, idx) : f32x4{0, 0, 0, 0};
+        const f32x4 nw = *reinterpret_cast<const f32x4 *>(a.nw + col);
+        f32x4 dnw, dnb;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float rstd = to_f32(ldv<T>(a.norm_rstd, a.norm == 3 ? col + j : row));
+            const NormGrad g = norm_grad(a.norm, e[j], pv[j], cv[j], rstd, nw[j], a.inv_n, a.inv_m);
+            dp[j] = g.d_prenorm;
+            dnw[j] = g.dnw;
+            dnb[j] = g.dnb;
+        }
+        *reinterpret_cast<f32x4 *>(a.d_norm_w + idx) = dnw;
+        *reinterpret_cast<f32x4 *>(a.d_norm_b + idx) = dnb;
+    }
+    dp = dp * a.loss_scale;
+    *reinterpret_cast<f32x4 *>(a.d_prenorm + idx) = dp;
+    if (a.d_prenorm_h) store4<half_t>(a.d_prenorm_h, idx, dp);
+}
+
+template <typename T> __global__ void __launch_bounds__(256) output_error_vec_kernel(ErrArgs a) {
+    const uint32_t nv = a.n >> 2, total = a.rows * nv;
+    for (uint32_t q = blockIdx.x * blockDim.x + threadIdx.x; q < total; q += gridDim.x * blockDim.x) {
+        const uint32_t row = q / nv, col = (q - row * nv) << 2;
+        const uint64_t idx = (uint64_t)row * a.n + col;
+        const f32x4 out = load4<T>(a.out, idx), tg = load4<T>(a.target, idx), pre = load4<T>(a.preact, idx);
+        f32x4 e;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float o = activation(a.act, out[j], a.leaky);
+            float ej = 0.0f;
+            if (a.loss == 0) {
+                ej = activation_derivative(a.act, o - tg[j], o, pre[j], a.leaky);
+            } else if ((a.loss == 1 && a.act == 5) || (a.loss == 2 && a.act == 1)) {
+                ej = o - tg[j];
+            }
+            e[j] = ej;
+        }
+        write_err4<T>(a, idx, row, col, e);
+    }
+}
+
+template <typename T> __global__ void __launch_bounds__(256) error_from_sum_vec_kernel(ErrArgs a) {
+    const uint32_t nv = a.n >> 2, total = a.rows * nv;
+    for (uint32_t q = blockIdx.x * blockDim.x + threadIdx.x; q < total; q += gridDim.x * blockDim.x) {
+        const uint32_t row = q / nv, col = (q - row * nv) << 2;
+        const uint64_t idx = (uint64_t)row * a.n + col;
+        const f32x4 s = *reinterpret_cast<const f32x4 *>(a.s + idx);
+        const f32x4 pd = load4<T>(a.predrop, idx), pa = load4<T>(a.preact, idx), mk = load4<T>(a.mask, idx);
+        f32x4 e;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) e[j] = mk[j] * activation_derivative(a.act, s[j], pd[j], pa[j], a.leaky);
+        write_err4<T>(a, idx, row, col, e);
+    }
+}
+
+static bool a16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+static bool err_vec_ok(const ErrArgs &a, bool from_sum) {
+    if ((a.n & 3u) != 0 || (uint64_t)a.rows * a.n >= (1ull << 32)) return false;
+    const void *ptrs[] = {a.grad, a.d_prenorm, a.d_prenorm_h, a.preact, a.norm ? a.nw : nullptr,
+                          a.norm ? a.d_norm_w : nullptr, a.norm ? a.d_norm_b : nullptr,
+                          a.norm == 1 ? a.prenorm : nullptr, a.norm >= 2 ? a.centered : nullptr,
+                          from_sum ? a.s : a.out, from_sum ? a.predrop : a.target, from_sum ? a.mask : nullptr};
+    for (const void *p : ptrs)
+        if (p && !a16(p)) return false;
+    return true;
+}
+
 hipError_t launch_output_error(const ErrArgs &a, hipStream_t s) {
     const uint64_t total = (uint64_t)a.rows * a.n;
     if (total == 0) return hipSuccess;
-    if (a.dtype == 1)
+    if (err_vec_ok(a, false)) {
+        if (a.dtype == 1)
+            hipLaunchKernelGGL(output_error_vec_kernel<half_t>, grid_for(total / 4, 256), dim3(256), 0, s, a);
+        else
+            hipLaunchKernelGGL(output_error_vec_kernel<float>, grid_for(total / 4, 256), dim3(256), 0, s, a);
+    } else if (a.dtype == 1) {
         hipLaunchKernelGGL(output_error_kernel<half_t>, grid_for(total, 256), dim3(256), 0, s, a);
-    else
+    } else {
         hipLaunchKernelGGL(output_error_kernel<float>, grid_for(total, 256), dim3(256), 0, s, a);
+    }
     return hipGetLastError();
 }
 
 hipError_t launch_error_from_sum(const ErrArgs &a, hipStream_t s) {
     const uint64_t total = (uint64_t)a.rows * a.n;
     if (total == 0) return hipSuccess;
-    if (a.dtype == 1)
+    if (err_vec_ok(a, true)) {
+        if (a.dtype == 1)
+            hipLaunchKernelGGL(error_from_sum_vec_kernel<half_t>, grid_for(total / 4, 256), dim3(256), 0, s, a);
+        else
+            hipLaunchKernelGGL(error_from_sum_vec_kernel<float>, grid_for(total / 4, 256), dim3(256), 0, s, a);
+    } else if (a.dtype == 1) {
         hipLaunchKernelGGL(error_from_sum_kernel<half_t>, grid_for(total, 256), dim3(256), 0, s, a);
-    else
+    } else {
         hipLaunchKernelGGL(error_from_sum_kernel<float>, grid_for(total, 256), dim3(256), 0, s, a);
+    }
     return hipGetLastError();
 }
 
@@ -308,14 +398,25 @@ __global__ void __launch_bounds__(256) colsum_kernel(VecOptArgs a) {
     }
 }
 
+// 64 columns per workgroup, 4 lanes per column: lane j sums the partials of
+// splits j, j+4, ... in order, then the four are added in a fixed order.
 template <typename T> __global__ void __launch_bounds__(256) vec_opt_kernel(VecOptArgs a) {
-    const uint32_t col = blockIdx.x * 256 + threadIdx.x;
-    if (col >= a.n) return;
+    __shared__ float red[3][4][64];
+    const uint32_t cl = threadIdx.x & 63u, j = threadIdx.x >> 6;
+    const uint32_t col = blockIdx.x * 64 + cl;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        float s = 0.0f;
+        if (a.enabled[k] && col < a.n)
+            for (uint32_t sp = j; sp < a.splits; sp += 4) s += a.partials[((uint64_t)sp * 3 + k) * a.n + col];
+        red[k][j][cl] = s;
+    }
+    __syncthreads();
+    if (j != 0 || col >= a.n) return;
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
         if (!a.enabled[k]) continue;
-        float s = 0.0f;
-        for (uint32_t sp = 0; sp < a.splits; ++sp) s += a.partials[((uint64_t)sp * 3 + k) * a.n + col];
+        const float s = (red[k][0][cl] + red[k][1][cl]) + (red[k][2][cl] + red[k][3][cl]);
         float p = a.master[k][col], v = a.dv[k][col], mm = a.dm[k][col];
         optimiser_step(p, v, mm, s * kLossScaleInv, a.inv_m, a.lr, a.clamp, a.opt[k], 0, 0.0f, false);
         a.master[k][col] = p;
@@ -325,18 +426,62 @@ template <typename T> __global__ void __launch_bounds__(256) vec_opt_kernel(VecO
     }
 }
 
+// Vector column sums: a thread owns 4 consecutive columns (one 16-byte load per
+// row); the row range of its split is walked 4 rows at a time for loads in flight.
+__global__ void __launch_bounds__(256) colsum_vec_kernel(VecOptArgs a) {
+    const uint32_t c = (blockIdx.x * 256 + threadIdx.x) * 4;
+    if (c >= a.n) return;
+    const uint32_t per = (a.rows + a.splits - 1) / a.splits;
+    const uint32_t r0 = blockIdx.y * per;
+    const uint32_t r1 = min(a.rows, r0 + per);
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        if (!a.src[k]) continue;
+        const float *src = a.src[k] + c;
+        f32x4 acc = {0, 0, 0, 0};
+        uint32_t r = r0;
+        for (; r + 4 <= r1; r += 4) {
+            const f32x4 v0 = *reinterpret_cast<const f32x4 *>(src + (uint64_t)r * a.n);
+            const f32x4 v1 = *reinterpret_cast<const f32x4 *>(src + (uint64_t)(r + 1) * a.n);
+            const f32x4 v2 = *reinterpret_cast<const f32x4 *>(src + (uint64_t)(r + 2) * a.n);
+            const f32x4 v3 = *reinterpret_cast<const f32x4 *>(src + (uint64_t)(r + 3) * a.n);
+            acc += v0;
+            acc += v1;
+            acc += v2;
+            acc += v3;
+        }
+        for (; r < r1; ++r) acc += *reinterpret_cast<const f32x4 *>(src + (uint64_t)r * a.n);
+        *reinterpret_cast<f32x4 *>(a.partials + ((uint64_t)blockIdx.y * 3 + k) * a.n + c) = acc;
+    }
+}
+
 hipError_t launch_colsum(const VecOptArgs &a, hipStream_t s) {
     if (a.n == 0) return hipSuccess;
-    hipLaunchKernelGGL(colsum_kernel, dim3(cdiv(a.n, 256), a.splits), dim3(256), 0, s, a);
+    bool vec = (a.n & 3u) == 0 && a16(a.partials);
+    for (int k = 0; k < 3; ++k)
+        if (a.src[k] && !a16(a.src[k])) vec = false;
+    if (vec)
+        hipLaunchKernelGGL(colsum_vec_kernel, dim3(cdiv(a.n, 1024), a.splits), dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL(colsum_kernel, dim3(cdiv(a.n, 256), a.splits), dim3(256), 0, s, a);
     return hipGetLastError();
+}
+
+uint32_t colsum_splits(uint32_t rows, uint32_t n) {
+    const uint32_t col_blocks = (n & 3u) == 0 ? cdiv(n, 1024) : cdiv(n, 256);
+    uint32_t sp = cdiv(1024, col_blocks);
+    const uint32_t cap = rows / 16 > 0 ? rows / 16 : 1;
+    if (sp > cap) sp = cap;
+    if (sp > 256) sp = 256;
+    return sp < 1 ? 1 : sp;
 }
 
 hipError_t launch_vec_opt(const VecOptArgs &a, hipStream_t s) {
     if (a.n == 0) return hipSuccess;
     if (a.dtype == 1)
-        hipLaunchKernelGGL(vec_opt_kernel<half_t>, dim3(cdiv(a.n, 256)), dim3(256), 0, s, a);
+        hipLaunchKernelGGL(vec_opt_kernel<half_t>, dim3(cdiv(a.n, 64)), dim3(256), 0, s, a);
     else
-        hipLaunchKernelGGL(vec_opt_kernel<float>, dim3(cdiv(a.n, 256)), dim3(256), 0, s, a);
+        hipLaunchKernelGGL(vec_opt_kernel<float>, dim3(cdiv(a.n, 64)), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
@@ -365,6 +510,47 @@ hipError_t launch_dw_reduce_opt(const DwReduceArgs &a, hipStream_t s) {
         hipLaunchKernelGGL(dw_reduce_opt_kernel<half_t>, grid_for(total, 256), dim3(256), 0, s, a);
     else
         hipLaunchKernelGGL(dw_reduce_opt_kernel<float>, grid_for(total, 256), dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+// ---- fp16 transpose (64 x 64 LDS tiles) ---------------------------------------------------
+// out[c][r] = in[r][c]; in is [rows x cols] (leading dim ld_in), out is [cols x rows]
+// (leading dim ld_out).  Loads are 16-byte row chunks; stores are 16-byte column
+// chunks gathered from LDS.  rows, cols, ld_in, ld_out are multiples of 8.
+__global__ void __launch_bounds__(256) transpose_h_kernel(const half_t *__restrict__ in, half_t *__restrict__ out,
+                                                          uint32_t rows, uint32_t cols, uint32_t ld_in,
+                                                          uint32_t ld_out) {
+    __shared__ half_t tile[64][64 + 8];
+    const uint32_t r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+    const uint32_t t = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t q = t + i * 256;              // 512 chunks of 8 halves
+        const uint32_t r = q >> 3, c = (q & 7u) * 8;
+        u32x4_t v = {0, 0, 0, 0};
+        if (r0 + r < rows && c0 + c < cols)
+            v = *reinterpret_cast<const u32x4_t *>(in + (uint64_t)(r0 + r) * ld_in + c0 + c);
+        *reinterpret_cast<u32x4_t *>(&tile[r][c]) = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t q = t + i * 256;
+        const uint32_t oc = q >> 3, orr = (q & 7u) * 8;   // out row = in col, out col = in row
+        if (c0 + oc >= cols || r0 + orr >= rows) continue;
+        half_t h[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) h[e] = tile[orr + e][oc];
+        *reinterpret_cast<u32x4_t *>(out + (uint64_t)(c0 + oc) * ld_out + r0 + orr) = __builtin_bit_cast(u32x4_t, h);
+    }
+}
+
+hipError_t launch_transpose_h(const void *in, void *out, uint32_t rows, uint32_t cols, uint32_t ld_in,
+                              uint32_t ld_out, hipStream_t s) {
+    if (rows == 0 || cols == 0) return hipSuccess;
+    hipLaunchKernelGGL(transpose_h_kernel, dim3(cdiv(cols, 64), cdiv(rows, 64)), dim3(256), 0, s,
+                       reinterpret_cast<const half_t *>(in), reinterpret_cast<half_t *>(out), rows, cols, ld_in,
+                       ld_out);
     return hipGetLastError();
 }
 

@@ -20,6 +20,34 @@ template <typename T> struct EpiFwdK {
     __device__ __forceinline__ static void apply(const FwdEpi &e, const GemmShape &sh, uint32_t m, uint32_t n,
                                                  floatx4 v, uint32_t) {
         if (m >= sh.M) return;
+        if (n + 3 < sh.N && (e.ldc & 3u) == 0) {
+            // 4 consecutive columns: one 8-byte (fp16) / 16-byte (fp32) access per tensor
+            const uint64_t idx = (uint64_t)m * e.ldc + n;
+            f32x4 z = v;
+            if (e.bias) z = z + load4<T>(e.bias, n);
+            store4<T>(e.z_out, idx, z);
+            if (!e.fuse_act) return;
+            const f32x4 zt = round4<T>(z);
+            f32x4 a;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) a[j] = activation(e.act, zt[j], e.leaky);
+            store4<T>(e.predrop, idx, a);
+            if (e.use_dropout) {
+                const float scale = 1.0f / (1.0f - e.p);
+                f32x4 mk, o;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const bool keep = dropout_u(n + j, m, e.seed + m * 7u) >= e.p;
+                    mk[j] = keep ? scale : 0.0f;
+                    o[j] = keep ? a[j] * scale : 0.0f;
+                }
+                store4<T>(e.mask, idx, mk);
+                store4<T>(e.out, idx, o);
+            } else {
+                store4<T>(e.out, idx, a);
+            }
+            return;
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const uint32_t c = n + j;
@@ -55,6 +83,34 @@ template <typename T> struct EpiHiddenK {
     __device__ __forceinline__ static void apply(const HiddenEpi &e, const GemmShape &sh, uint32_t m,
                                                  uint32_t n, floatx4 v, uint32_t) {
         if (m >= sh.M) return;
+        if (n + 3 < sh.N && (e.ldc & 3u) == 0) {
+            const uint64_t idx = (uint64_t)m * e.ldc + n;
+            const f32x4 pd = load4<T>(e.predrop, idx), pa = load4<T>(e.preact, idx), mk = load4<T>(e.mask, idx);
+            f32x4 err;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) err[j] = mk[j] * activation_derivative(e.act, v[j], pd[j], pa[j], e.leaky);
+            *reinterpret_cast<f32x4 *>(e.grad + idx) = err;
+            f32x4 dp = err;
+            if (e.norm) {
+                const f32x4 pv = e.norm == 1 ? load4<T>(e.prenorm, idx) : f32x4{0, 0, 0, 0};
+                const f32x4 cv = e.norm >= 2 ? load4<T>(e.centered, idx) : f32x4{0, 0, 0, 0};
+                f32x4 dnw, dnb;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float rstd = to_f32(ld_t<T>(e.norm_rstd, e.norm == 3 ? n + j : m));
+                    const NormGrad g = norm_grad(e.norm, err[j], pv[j], cv[j], rstd, e.nw[n + j], e.inv_n, e.inv_m);
+                    dp[j] = g.d_prenorm;
+                    dnw[j] = g.dnw;
+                    dnb[j] = g.dnb;
+                }
+                *reinterpret_cast<f32x4 *>(e.d_norm_w + idx) = dnw;
+                *reinterpret_cast<f32x4 *>(e.d_norm_b + idx) = dnb;
+            }
+            dp = dp * e.loss_scale;
+            *reinterpret_cast<f32x4 *>(e.d_prenorm + idx) = dp;
+            if (e.d_prenorm_h) store4<half_t>(e.d_prenorm_h, idx, dp);
+            return;
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const uint32_t c = n + j;
@@ -206,11 +262,19 @@ static hipError_t dispatch_vec(const GemmLaunch &g, const typename Epi::Params &
 template <class C> static hipError_t dispatch_op(const GemmLaunch &g, hipStream_t s) {
     typedef typename C::type T;
     switch (g.op) {
-    case Op::Fwd: return dispatch_vec<C, true, false, EpiFwdK<T>>(g, g.fwd, s);
+    // forward on W or on a transposed copy of W
+    case Op::Fwd:
+        return g.b_kcontig ? dispatch_vec<C, true, true, EpiFwdK<T>>(g, g.fwd, s)
+                           : dispatch_vec<C, true, false, EpiFwdK<T>>(g, g.fwd, s);
     case Op::Hidden: return dispatch_vec<C, true, true, EpiHiddenK<T>>(g, g.hid, s);
     case Op::InputGrad: return dispatch_vec<C, true, true, EpiStoreK>(g, g.st, s);
-    case Op::DwPartial: return dispatch_vec<C, false, false, EpiStoreK>(g, g.st, s);
-    case Op::DwOpt: return dispatch_vec<C, false, false, EpiOptK<T>>(g, g.opt, s);
+    // dW also runs on transposed copies of X and dP (both k-contiguous)
+    case Op::DwPartial:
+        return g.a_kcontig ? dispatch_vec<C, true, true, EpiStoreK>(g, g.st, s)
+                           : dispatch_vec<C, false, false, EpiStoreK>(g, g.st, s);
+    case Op::DwOpt:
+        return g.a_kcontig ? dispatch_vec<C, true, true, EpiOptK<T>>(g, g.opt, s)
+                           : dispatch_vec<C, false, false, EpiOptK<T>>(g, g.opt, s);
     }
     return hipErrorInvalidValue;
 }

@@ -115,6 +115,8 @@ struct VecOptArgs {
     float lr, clamp, inv_m;
 };
 hipError_t launch_colsum(const VecOptArgs &a, hipStream_t s);
+// Row splits for launch_colsum so the grid has ~1024 workgroups.
+uint32_t colsum_splits(uint32_t rows, uint32_t n);
 hipError_t launch_vec_opt(const VecOptArgs &a, hipStream_t s);
 
 // Split-K dW reduction + W optimiser.
@@ -124,5 +126,10 @@ struct DwReduceArgs {
     OptEpi e;
 };
 hipError_t launch_dw_reduce_opt(const DwReduceArgs &a, hipStream_t s);
+
+// fp16 transpose: out [cols x rows] (ld_out) = in [rows x cols] (ld_in)^T.
+// rows, cols, ld_in, ld_out multiples of 8; both buffers 16-byte aligned.
+hipError_t launch_transpose_h(const void *in, void *out, uint32_t rows, uint32_t cols, uint32_t ld_in,
+                              uint32_t ld_out, hipStream_t s);
 
 }  // namespace skl

@@ -74,7 +74,7 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 bool use_transposed_operands(uint32_t dtype, uint32_t M, uint32_t N, uint32_t K, uint32_t ld) {
     if (dtype != SKL_F16) return false;
     if ((M | N | K | ld) & 7u) return false;
-    return gemm_tiles(dtype, M, N) >= 192 && ((M + 255) / 256) * ((N + 255) / 256) >= 192;
+    return gemm_large_tile(dtype, M, N);
 }
 
 // Common configuration checks of a block descriptor.

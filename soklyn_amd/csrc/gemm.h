@@ -5,24 +5,30 @@
 //   B(k, n) = B_KCONTIG ? B[n * ldb + k] : B[k * ldb + n]
 //
 // The three DenseBlock contractions map onto it as
-//   forward  Z  = X . W        A = X  (k-contig),  B = W   (n-contig)
+//   forward  Z  = X . W        A = X  (k-contig),  B = W   (n-contig, or W^T k-contig)
 //   dX       s  = dP . W^T     A = dP (k-contig),  B = W   (k-contig)
-//   dW       dW = X^T . dP     A = X  (m-contig),  B = dP  (n-contig)
+//   dW       dW = X^T . dP     A = X  (m-contig),  B = dP  (n-contig, or both transposed: k-contig)
 //
 // Design:
 //  * Block tile BM x BN x BK, WM x WN waves, each wave owns a (BM/WM) x (BN/WN)
 //    sub-tile built from 32x32 MFMA tiles (v_mfma_f32_32x32x16_f16 for fp16,
 //    v_mfma_f32_32x32x2_f32 for fp32).
 //  * LDS holds both operands k-contiguous in 16-byte chunks (8 halves / 4
-//    floats), double buffered, with chunk index XOR-swizzled by
-//    (row ^ row >> 3) & 7 so fragment reads and transposed staging writes of
-//    8 consecutive lanes hit 8 distinct chunks.
+//    floats per chunk, 8 chunks per row), double buffered.  When both
+//    operands are k-contiguous in HBM, rows are padded to 9 chunks: 8
+//    consecutive rows start 9 chunks apart (conflict-free 16-byte reads) and
+//    every fragment / staging address is a per-lane base plus a compile-time
+//    offset.  Otherwise the 8 chunks of a row are XOR-swizzled by
+//    (row ^ row >> 3) & 7, which also keeps the transposed staging writes
+//    conflict-free.
 //  * Operands that are not k-contiguous in HBM are transposed in registers
-//    while staging (8x8 halves with v_perm_b32, 4x4 floats by renaming), so
-//    every fragment read is one 16-byte ds_read.
+//    while staging (8x8 halves with v_perm_b32, 4x4 floats by renaming).
+//  * Interior tiles with a whole number of K-tiles run a loop with no bounds
+//    checks at all; edge tiles run the guarded loop.
 //  * The MFMA is issued with the operands swapped (B fragment as the "A"
 //    input), so each lane ends up owning 4 consecutive output columns of one
-//    row: the epilogue reads/writes 16-byte fp32 or 8-byte fp16 vectors.
+//    row; the accumulator tile then goes through LDS to a compact epilogue
+//    loop in which consecutive lanes own consecutive 4-column groups.
 //  * Workgroup -> tile mapping is XCD-aware: consecutive tiles of an
 //    8 x TN group land on one XCD so they share that XCD's L2.
 //  * Optional split-K over blockIdx.z (partials go to a workspace).
@@ -47,10 +53,18 @@ struct GemmShape {
     uint32_t tiles_m, tiles_n;
 };
 
-// Physical 16-byte chunk of (row, kc) in a k-contiguous LDS tile of 8 chunks per row.
-__device__ __forceinline__ uint32_t swz(uint32_t row, uint32_t kc) {
-    return row * 8u + (kc ^ ((row ^ (row >> 3)) & 7u));
-}
+// LDS chunk index of (row, kc) in a k-contiguous tile.
+template <bool PADDED> struct LdsLayout;
+template <> struct LdsLayout<true> {
+    static constexpr int PITCH = 9;   // chunks per row (8 data + 1 pad)
+    __device__ __forceinline__ static uint32_t idx(uint32_t row, uint32_t kc) { return row * 9u + kc; }
+};
+template <> struct LdsLayout<false> {
+    static constexpr int PITCH = 8;
+    __device__ __forceinline__ static uint32_t idx(uint32_t row, uint32_t kc) {
+        return row * 8u + (kc ^ ((row ^ (row >> 3)) & 7u));
+    }
+};
 
 template <typename T> struct Mfma;
 
@@ -102,8 +116,10 @@ __device__ __forceinline__ void transpose4x4(const u32x4 (&in)[4], u32x4 (&out)[
 //  else   : global element (row, k) at p[k * ld + row]
 // VECOK: ld, the contiguous extent and the base are multiples of VEC
 // elements, so whole 16-byte chunks are either fully in range or fully out.
-template <typename T, int ROWS, int BK, int NT, bool KCONTIG, bool VECOK>
+// GUARD = false: the caller guarantees the whole tile is in range.
+template <typename T, int ROWS, int BK, int NT, bool KCONTIG, bool VECOK, bool PADDED>
 struct Stager {
+    typedef LdsLayout<PADDED> L;
     static constexpr int VEC = Mfma<T>::VEC;
     static constexpr int KC = BK / VEC;                 // chunks per LDS row (8)
     static_assert(KC == 8, "LDS rows must hold 8 chunks");
@@ -139,6 +155,7 @@ struct Stager {
         return __builtin_bit_cast(u32x4, v);
     }
 
+    template <bool GUARD>
     __device__ __forceinline__ void load(const T *p, uint32_t ld, uint32_t row0, uint32_t k0, uint32_t rows,
                                          uint32_t kmax, uint32_t tid) {
         if constexpr (KCONTIG) {
@@ -147,10 +164,12 @@ struct Stager {
                 const uint32_t c = tid + i * NT;
                 const uint32_t row = row0 + c / KC;
                 const uint32_t k = k0 + (c % KC) * VEC;
-                if constexpr (VECOK) {
+                if constexpr (!VECOK) {
+                    r[i] = gather(p, ld, row, k, rows, kmax);
+                } else if constexpr (GUARD) {
                     r[i] = (row < rows && k < kmax) ? load_chunk(p, (uint64_t)row * ld + k) : u32x4{0, 0, 0, 0};
                 } else {
-                    r[i] = gather(p, ld, row, k, rows, kmax);
+                    r[i] = load_chunk(p, (uint64_t)row * ld + k);
                 }
             }
         } else {
@@ -164,11 +183,13 @@ struct Stager {
 #pragma unroll
                 for (int e = 0; e < VEC; ++e) {
                     const uint32_t k = k0 + kb * VEC + e;
-                    if constexpr (VECOK) {
+                    if constexpr (!VECOK) {
+                        r[b * VEC + e] = gather(p, ld, row, k, rows, kmax);
+                    } else if constexpr (GUARD) {
                         r[b * VEC + e] = (row < rows && k < kmax) ? load_chunk(p, (uint64_t)k * ld + row)
                                                                    : u32x4{0, 0, 0, 0};
                     } else {
-                        r[b * VEC + e] = gather(p, ld, row, k, rows, kmax);
+                        r[b * VEC + e] = load_chunk(p, (uint64_t)k * ld + row);
                     }
                 }
             }
@@ -180,7 +201,7 @@ struct Stager {
 #pragma unroll
             for (int i = 0; i < PER; ++i) {
                 const uint32_t c = tid + i * NT;
-                lds[swz(c / KC, c % KC)] = r[i];
+                lds[L::idx(c / KC, c % KC)] = r[i];
             }
         } else {
             if (NBLK < NT && tid >= (uint32_t)BACTIVE) return;
@@ -198,7 +219,7 @@ struct Stager {
                     transpose4x4(in, t);
                 }
 #pragma unroll
-                for (int e = 0; e < VEC; ++e) lds[swz(rb * VEC + e, kb)] = t[e];
+                for (int e = 0; e < VEC; ++e) lds[L::idx(rb * VEC + e, kb)] = t[e];
             }
         }
     }
@@ -221,6 +242,93 @@ __device__ __forceinline__ void tile_coords(uint32_t wg, uint32_t tiles_m, uint3
     tn = in_group / gsize;
 }
 
+// The K loop: double-buffered LDS, register prefetch one K-tile ahead,
+// unrolled by two so each half works on a compile-time buffer.
+template <typename T, int BM, int BN, int BK, int WM, int WN, bool A_KCONTIG, bool B_KCONTIG, bool VECOK,
+          bool PADDED>
+struct MainLoop {
+    static constexpr int NT = WM * WN * 64;
+    static constexpr int VEC = Mfma<T>::VEC;
+    static constexpr int KSTEP = Mfma<T>::KSTEP;
+    static constexpr int TWM = BM / WM, TWN = BN / WN;
+    static constexpr int MT = TWM / 32, NTL = TWN / 32;
+    static constexpr int PITCH = LdsLayout<PADDED>::PITCH;
+    static constexpr int A_CHUNKS = BM * PITCH, B_CHUNKS = BN * PITCH;
+    static constexpr int STAGE = A_CHUNKS + B_CHUNKS;
+    typedef Stager<T, BM, BK, NT, A_KCONTIG, VECOK, PADDED> SA;
+    typedef Stager<T, BN, BK, NT, B_KCONTIG, VECOK, PADDED> SB;
+
+    template <int BUF>
+    __device__ __forceinline__ static void compute(const u32x4 *smem, floatx16 (&acc)[MT][NTL], uint32_t wm,
+                                                   uint32_t wn, uint32_t frow, uint32_t fhalf) {
+        const u32x4 *as = smem + BUF * STAGE;
+        const u32x4 *bs = as + A_CHUNKS;
+#pragma unroll
+        for (int ks = 0; ks < BK / KSTEP; ++ks) {
+            const uint32_t kc = (uint32_t)ks * 2u + fhalf;
+            u32x4 af[MT], bf[NTL];
+            if constexpr (PADDED) {
+                const u32x4 *ab = as + (wm * TWM + frow) * PITCH + fhalf;
+                const u32x4 *bb = bs + (wn * TWN + frow) * PITCH + fhalf;
+#pragma unroll
+                for (int i = 0; i < MT; ++i) af[i] = ab[i * 32 * PITCH + ks * 2];
+#pragma unroll
+                for (int j = 0; j < NTL; ++j) bf[j] = bb[j * 32 * PITCH + ks * 2];
+            } else {
+#pragma unroll
+                for (int i = 0; i < MT; ++i) af[i] = as[LdsLayout<false>::idx(wm * TWM + i * 32 + frow, kc)];
+#pragma unroll
+                for (int j = 0; j < NTL; ++j) bf[j] = bs[LdsLayout<false>::idx(wn * TWN + j * 32 + frow, kc)];
+            }
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int j = 0; j < NTL; ++j) Mfma<T>::run(acc[i][j], bf[j], af[i]);
+        }
+    }
+
+    template <bool GUARD, int BUF>
+    __device__ __forceinline__ static void step(u32x4 *smem, floatx16 (&acc)[MT][NTL], SA &sa, SB &sb,
+                                                const GemmShape &sh, const T *A, const T *B, uint32_t m0,
+                                                uint32_t n0, uint32_t kbeg, uint32_t kend, int kt, int nk,
+                                                uint32_t tid, uint32_t wm, uint32_t wn, uint32_t frow,
+                                                uint32_t fhalf) {
+        const bool more = kt + 1 < nk;
+        if (more) {
+            const uint32_t k0 = kbeg + (uint32_t)(kt + 1) * BK;
+            sa.template load<GUARD>(A, sh.lda, m0, k0, sh.M, kend, tid);
+            sb.template load<GUARD>(B, sh.ldb, n0, k0, sh.N, kend, tid);
+        }
+        compute<BUF>(smem, acc, wm, wn, frow, fhalf);
+        if (more) {
+            u32x4 *nxt = smem + (BUF ^ 1) * STAGE;
+            sa.store(nxt, tid);
+            sb.store(nxt + A_CHUNKS, tid);
+        }
+        __syncthreads();
+    }
+
+    template <bool GUARD>
+    __device__ __forceinline__ static void run(u32x4 *smem, floatx16 (&acc)[MT][NTL], const GemmShape &sh,
+                                               const T *A, const T *B, uint32_t m0, uint32_t n0, uint32_t kbeg,
+                                               uint32_t kend, int nk, uint32_t tid, uint32_t wm, uint32_t wn,
+                                               uint32_t frow, uint32_t fhalf) {
+        SA sa;
+        SB sb;
+        sa.template load<GUARD>(A, sh.lda, m0, kbeg, sh.M, kend, tid);
+        sb.template load<GUARD>(B, sh.ldb, n0, kbeg, sh.N, kend, tid);
+        sa.store(smem, tid);
+        sb.store(smem + A_CHUNKS, tid);
+        __syncthreads();
+        for (int kt = 0; kt < nk; kt += 2) {
+            step<GUARD, 0>(smem, acc, sa, sb, sh, A, B, m0, n0, kbeg, kend, kt, nk, tid, wm, wn, frow, fhalf);
+            if (kt + 1 < nk)
+                step<GUARD, 1>(smem, acc, sa, sb, sh, A, B, m0, n0, kbeg, kend, kt + 1, nk, tid, wm, wn, frow,
+                               fhalf);
+        }
+    }
+};
+
 // The GEMM kernel.  Epi provides:
 //   struct Params;
 //   static void apply(const Params&, const GemmShape&, uint32_t m, uint32_t n, floatx4 v, uint32_t split)
@@ -230,23 +338,22 @@ template <typename T, int BM, int BN, int BK, int WM, int WN, bool A_KCONTIG, bo
           class Epi>
 __global__ void __launch_bounds__(WM *WN * 64)
     gemm_kernel(GemmShape sh, const T *__restrict__ A, const T *__restrict__ B, typename Epi::Params ep) {
-    constexpr int NT = WM * WN * 64;
-    constexpr int VEC = Mfma<T>::VEC;
-    constexpr int KSTEP = Mfma<T>::KSTEP;
-    constexpr int TWM = BM / WM, TWN = BN / WN;   // wave tile
-    constexpr int MT = TWM / 32, NTL = TWN / 32;  // 32x32 tiles per wave
-    constexpr int A_CHUNKS = BM * BK / VEC, B_CHUNKS = BN * BK / VEC;
-    static_assert(BK / VEC == 8, "LDS row = 8 chunks");
-
-    constexpr int MAIN_CHUNKS = 2 * (A_CHUNKS + B_CHUNKS);
-    constexpr int EPI_CHUNKS = (WM * ((MT >= 2) ? 2 : 1) * 32 * (BN + 4)) / 4;
+    constexpr bool PADDED = A_KCONTIG && B_KCONTIG;
+    typedef MainLoop<T, BM, BN, BK, WM, WN, A_KCONTIG, B_KCONTIG, VECOK, PADDED> ML;
+    constexpr int NT = ML::NT;
+    constexpr int TWM = ML::TWM, TWN = ML::TWN;
+    constexpr int MT = ML::MT, NTL = ML::NTL;
+    constexpr int MAIN_CHUNKS = 2 * ML::STAGE;
+    constexpr int EPITCH = BN + 4;                      // floats per staged epilogue row (bank skew)
+    constexpr int EPI_CHUNKS = (WM * ((MT >= 2) ? 2 : 1) * 32 * EPITCH) / 4;
     __shared__ u32x4 smem[MAIN_CHUNKS > EPI_CHUNKS ? MAIN_CHUNKS : EPI_CHUNKS];
-    // buffer b: A tile at smem + b * (A_CHUNKS + B_CHUNKS), B tile right after it
 
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63u;
     const uint32_t wave = tid >> 6;
     const uint32_t wm = wave / WN, wn = wave % WN;
+    const uint32_t frow = lane & 31u;   // row within a 32-row MFMA tile
+    const uint32_t fhalf = lane >> 5;   // k lane-half
 
     uint32_t tm, tn;
     tile_coords(blockIdx.x, sh.tiles_m, sh.tiles_n, tm, tn);
@@ -254,9 +361,6 @@ __global__ void __launch_bounds__(WM *WN * 64)
     const uint32_t kbeg = blockIdx.z * sh.k_per_split;
     const uint32_t kend = min(sh.K, kbeg + sh.k_per_split);
     const int nk = kend > kbeg ? (int)((kend - kbeg + BK - 1) / BK) : 0;
-
-    Stager<T, BM, BK, NT, A_KCONTIG, VECOK> sa;
-    Stager<T, BN, BK, NT, B_KCONTIG, VECOK> sb;
 
     floatx16 acc[MT][NTL];
 #pragma unroll
@@ -267,44 +371,11 @@ __global__ void __launch_bounds__(WM *WN * 64)
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
     if (nk > 0) {
-        sa.load(A, sh.lda, m0, kbeg, sh.M, kend, tid);
-        sb.load(B, sh.ldb, n0, kbeg, sh.N, kend, tid);
-        sa.store(smem, tid);
-        sb.store(smem + A_CHUNKS, tid);
-        __syncthreads();
-    }
-
-    const uint32_t frow = lane & 31u;   // row within a 32-row MFMA tile
-    const uint32_t fhalf = lane >> 5;   // k lane-half
-
-    for (int kt = 0; kt < nk; ++kt) {
-        const int cur = kt & 1;
-        if (kt + 1 < nk) {
-            const uint32_t k0 = kbeg + (uint32_t)(kt + 1) * BK;
-            sa.load(A, sh.lda, m0, k0, sh.M, kend, tid);
-            sb.load(B, sh.ldb, n0, k0, sh.N, kend, tid);
-        }
-        const u32x4 *as = smem + cur * (A_CHUNKS + B_CHUNKS);
-        const u32x4 *bs = as + A_CHUNKS;
-#pragma unroll
-        for (int ks = 0; ks < BK / KSTEP; ++ks) {
-            const uint32_t kc = (uint32_t)ks * 2u + fhalf;
-            u32x4 af[MT], bf[NTL];
-#pragma unroll
-            for (int i = 0; i < MT; ++i) af[i] = as[swz(wm * TWM + i * 32 + frow, kc)];
-#pragma unroll
-            for (int j = 0; j < NTL; ++j) bf[j] = bs[swz(wn * TWN + j * 32 + frow, kc)];
-#pragma unroll
-            for (int i = 0; i < MT; ++i)
-#pragma unroll
-                for (int j = 0; j < NTL; ++j) Mfma<T>::run(acc[i][j], bf[j], af[i]);
-        }
-        if (kt + 1 < nk) {
-            u32x4 *nxt = smem + (cur ^ 1) * (A_CHUNKS + B_CHUNKS);
-            sa.store(nxt, tid);
-            sb.store(nxt + A_CHUNKS, tid);
-        }
-        __syncthreads();
+        const bool interior = m0 + BM <= sh.M && n0 + BN <= sh.N && (kend - kbeg) % BK == 0;
+        if (VECOK && interior)
+            ML::template run<false>(smem, acc, sh, A, B, m0, n0, kbeg, kend, nk, tid, wm, wn, frow, fhalf);
+        else
+            ML::template run<true>(smem, acc, sh, A, B, m0, n0, kbeg, kend, nk, tid, wm, wn, frow, fhalf);
     }
 
     // Epilogue.  The accumulator tile goes through LDS (in passes when it is
@@ -313,7 +384,6 @@ __global__ void __launch_bounds__(WM *WN * 64)
     // of a row: coalesced HBM traffic and no per-register code duplication.
     // Lane layout after the swapped MFMA: C[m][n..n+3] with
     // m = wave row + 32 i + (lane & 31), n = wave col + 32 j + 8 g + 4 (lane >> 5).
-    constexpr int EPITCH = BN + 4;                      // floats per staged row (bank skew)
     constexpr int ARENA = (int)(sizeof(smem) / 4);      // floats
     constexpr int MTP = (WM * MT * 32 * EPITCH <= ARENA) ? MT : (MT >= 2 ? 2 : 1);
     static_assert(MT % MTP == 0, "epilogue passes");

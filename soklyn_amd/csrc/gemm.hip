@@ -210,7 +210,6 @@ template <typename T, int BM, int BN, int BK, int WM, int WN> struct Cfg {
     typedef T type;
     static constexpr int bm = BM, bn = BN, bk = BK, wm = WM, wn = WN, nt = WM * WN * 64;
 };
-typedef Cfg<half_t, 256, 256, 64, 2, 2> CfgH256;     // 4 waves, 128x128 per wave, 1 wave / SIMD
 typedef Cfg<half_t, 256, 256, 64, 2, 4> CfgH256w8;   // 8 waves, 128x64 per wave, 2 waves / SIMD
 typedef Cfg<half_t, 128, 128, 64, 2, 2> CfgH128;
 typedef Cfg<float, 128, 128, 32, 2, 2> CfgF128;
@@ -279,12 +278,27 @@ template <class C> static hipError_t dispatch_op(const GemmLaunch &g, hipStream_
     return hipErrorInvalidValue;
 }
 
-uint32_t gemm_tiles(uint32_t dtype, uint32_t M, uint32_t N) {
-    if (dtype == 1) {
-        const uint32_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
-        if (t256 >= 192) return t256;
-        return ((M + 127) / 128) * ((N + 127) / 128);
+// The 256x256 tile only runs the all-k-contiguous layout (large fp16
+// problems are given transposed operands by the caller).
+template <class C> static hipError_t dispatch_kk(const GemmLaunch &g, hipStream_t s) {
+    typedef typename C::type T;
+    switch (g.op) {
+    case Op::Fwd: return dispatch_vec<C, true, true, EpiFwdK<T>>(g, g.fwd, s);
+    case Op::Hidden: return dispatch_vec<C, true, true, EpiHiddenK<T>>(g, g.hid, s);
+    case Op::InputGrad:
+    case Op::DwPartial: return dispatch_vec<C, true, true, EpiStoreK>(g, g.st, s);
+    case Op::DwOpt: return dispatch_vec<C, true, true, EpiOptK<T>>(g, g.opt, s);
     }
+    return hipErrorInvalidValue;
+}
+
+bool gemm_large_tile(uint32_t dtype, uint32_t M, uint32_t N) {
+    return dtype == 1 && ((M + 255) / 256) * ((N + 255) / 256) >= 192;
+}
+
+// Output tiles of the general (non-256) configuration; drives split-K.
+uint32_t gemm_tiles(uint32_t dtype, uint32_t M, uint32_t N) {
+    if (dtype == 1) return ((M + 127) / 128) * ((N + 127) / 128);
     const uint32_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
     if (t128 >= 192) return t128;
     return ((M + 63) / 64) * ((N + 63) / 64);
@@ -292,21 +306,11 @@ uint32_t gemm_tiles(uint32_t dtype, uint32_t M, uint32_t N) {
 
 uint32_t gemm_bk(uint32_t dtype) { return dtype == 1 ? 64 : 32; }
 
-// Large fp16 tile variant: SOKLYN_GEMM_WAVES=4|8 (tuning override; default 8).
-static int large_tile_waves() {
-    static int w = [] {
-        const char *e = getenv("SOKLYN_GEMM_WAVES");
-        return (e && atoi(e) == 4) ? 4 : 8;
-    }();
-    return w;
-}
-
 hipError_t launch_gemm(const GemmLaunch &g, hipStream_t s) {
     if (g.M == 0 || g.N == 0) return hipSuccess;
     if (g.dtype == 1) {
-        const uint32_t t256 = ((g.M + 255) / 256) * ((g.N + 255) / 256);
-        if (t256 < 192) return dispatch_op<CfgH128>(g, s);
-        return large_tile_waves() == 4 ? dispatch_op<CfgH256>(g, s) : dispatch_op<CfgH256w8>(g, s);
+        if (gemm_large_tile(g.dtype, g.M, g.N) && g.a_kcontig && g.b_kcontig) return dispatch_kk<CfgH256w8>(g, s);
+        return dispatch_op<CfgH128>(g, s);
     }
     const uint32_t t128 = ((g.M + 127) / 128) * ((g.N + 127) / 128);
     return t128 >= 192 ? dispatch_op<CfgF128>(g, s) : dispatch_op<CfgF64>(g, s);

@@ -70,6 +70,8 @@ struct GemmLaunch {
 hipError_t launch_gemm(const GemmLaunch &g, hipStream_t stream);
 // Number of output tiles the launcher would use (for split-K sizing).
 uint32_t gemm_tiles(uint32_t dtype, uint32_t M, uint32_t N);
+// True when an fp16 GEMM of this output size uses the 256x256 tile (k-contiguous operands only).
+bool gemm_large_tile(uint32_t dtype, uint32_t M, uint32_t N);
 uint32_t gemm_bk(uint32_t dtype);
 
 // ---- element-wise / row / column kernels -------------------------------------

@@ -3,6 +3,7 @@
 #include <stdlib.h>
 
 #include "gemm.h"
+#include "gemm_dma.h"
 #include "launch.h"
 
 namespace skl {
@@ -306,9 +307,56 @@ uint32_t gemm_tiles(uint32_t dtype, uint32_t M, uint32_t N) {
 
 uint32_t gemm_bk(uint32_t dtype) { return dtype == 1 ? 64 : 32; }
 
+// The deep-pipelined DMA kernel: fp16, k-contiguous operands, whole 256x256
+// tiles, K a multiple of 32, 32-bit operand offsets.  SOKLYN_GEMM_DMA=0
+// selects the register-staged kernel instead (A/B comparisons).
+static bool dma_enabled() {
+    static bool on = [] {
+        const char *e = getenv("SOKLYN_GEMM_DMA");
+        return !(e && atoi(e) == 0);
+    }();
+    return on;
+}
+
+static bool dma_ok(const GemmLaunch &g) {
+    if (!dma_enabled() || g.dtype != 1 || !g.a_kcontig || !g.b_kcontig) return false;
+    if ((g.M % 256) || (g.N % 256) || (g.K % 64) || g.K == 0 || (g.splits && g.splits != 1)) return false;
+    if (!vec_ok(g, 8)) return false;
+    return (uint64_t)g.M * g.lda * 2 < (1ull << 32) && (uint64_t)g.N * g.ldb * 2 < (1ull << 32);
+}
+
+template <class Epi> static hipError_t run_dma(const GemmLaunch &g, const typename Epi::Params &p, hipStream_t s) {
+    GemmShape sh{};
+    sh.M = g.M;
+    sh.N = g.N;
+    sh.K = g.K;
+    sh.lda = g.lda;
+    sh.ldb = g.ldb;
+    sh.k_per_split = g.K;
+    sh.tiles_m = g.M / 256;
+    sh.tiles_n = g.N / 256;
+    const dim3 grid(sh.tiles_m * sh.tiles_n);
+    const half_t *A = reinterpret_cast<const half_t *>(g.A);
+    const half_t *B = reinterpret_cast<const half_t *>(g.B);
+    hipLaunchKernelGGL((gemm_dma_kernel<Epi>), grid, dim3(Dma64::NT), 0, s, sh, A, B, p);
+    return hipGetLastError();
+}
+
+static hipError_t dispatch_dma(const GemmLaunch &g, hipStream_t s) {
+    switch (g.op) {
+    case Op::Fwd: return run_dma<EpiFwdK<half_t>>(g, g.fwd, s);
+    case Op::Hidden: return run_dma<EpiHiddenK<half_t>>(g, g.hid, s);
+    case Op::InputGrad:
+    case Op::DwPartial: return run_dma<EpiStoreK>(g, g.st, s);
+    case Op::DwOpt: return run_dma<EpiOptK<half_t>>(g, g.opt, s);
+    }
+    return hipErrorInvalidValue;
+}
+
 hipError_t launch_gemm(const GemmLaunch &g, hipStream_t s) {
     if (g.M == 0 || g.N == 0) return hipSuccess;
     if (g.dtype == 1) {
+        if (gemm_large_tile(g.dtype, g.M, g.N) && dma_ok(g)) return dispatch_dma(g, s);
         if (gemm_large_tile(g.dtype, g.M, g.N) && g.a_kcontig && g.b_kcontig) return dispatch_kk<CfgH256w8>(g, s);
         return dispatch_op<CfgH128>(g, s);
     }

@@ -16,37 +16,56 @@ template <typename T> __device__ __forceinline__ void st_t(void *p, uint64_t i, 
 }
 
 // ---- forward: bias (+ act + dropout) ------------------------------------------
+//
+// Every epilogue has a whole-vector form in three parts, so a caller can batch
+// the global loads of many 4-column groups before computing any of them:
+//   column(e, n)        per-column operands of columns n..n+3 (loaded once)
+//   load(e, idx, m, p)  per-element operands of row m, columns n..n+3
+//   finish(e, idx, m, n, v, col, p)  compute from the fp32 accumulators v, store
+// apply() handles one 4-column group, including ragged edges.
 template <typename T> struct EpiFwdK {
     typedef FwdEpi Params;
+    __device__ __forceinline__ static uint32_t ldc(const FwdEpi &e) { return e.ldc; }
+    struct Col { f32x4 bias; };
+    struct Pre {};
+    __device__ __forceinline__ static Col column(const FwdEpi &e, uint32_t n) {
+        Col c;
+        c.bias = e.bias ? load4<T>(e.bias, n) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        return c;
+    }
+    __device__ __forceinline__ static void load(const FwdEpi &, uint64_t, uint32_t, Pre &) {}
+    __device__ __forceinline__ static void finish(const FwdEpi &e, uint64_t idx, uint32_t m, uint32_t n, floatx4 v,
+                                                  const Col &col, const Pre &) {
+        // 4 consecutive columns: one 8-byte (fp16) / 16-byte (fp32) access per tensor
+        f32x4 z = v;
+        if (e.bias) z = z + col.bias;
+        store4<T>(e.z_out, idx, z);
+        if (!e.fuse_act) return;
+        const f32x4 zt = round4<T>(z);
+        f32x4 a;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a[j] = activation(e.act, zt[j], e.leaky);
+        store4<T>(e.predrop, idx, a);
+        if (e.use_dropout) {
+            const float scale = 1.0f / (1.0f - e.p);
+            f32x4 mk, o;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const bool keep = dropout_u(n + j, m, e.seed + m * 7u) >= e.p;
+                mk[j] = keep ? scale : 0.0f;
+                o[j] = keep ? a[j] * scale : 0.0f;
+            }
+            store4<T>(e.mask, idx, mk);
+            store4<T>(e.out, idx, o);
+        } else {
+            store4<T>(e.out, idx, a);
+        }
+    }
     __device__ __forceinline__ static void apply(const FwdEpi &e, const GemmShape &sh, uint32_t m, uint32_t n,
                                                  floatx4 v, uint32_t) {
         if (m >= sh.M) return;
         if (n + 3 < sh.N && (e.ldc & 3u) == 0) {
-            // 4 consecutive columns: one 8-byte (fp16) / 16-byte (fp32) access per tensor
-            const uint64_t idx = (uint64_t)m * e.ldc + n;
-            f32x4 z = v;
-            if (e.bias) z = z + load4<T>(e.bias, n);
-            store4<T>(e.z_out, idx, z);
-            if (!e.fuse_act) return;
-            const f32x4 zt = round4<T>(z);
-            f32x4 a;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) a[j] = activation(e.act, zt[j], e.leaky);
-            store4<T>(e.predrop, idx, a);
-            if (e.use_dropout) {
-                const float scale = 1.0f / (1.0f - e.p);
-                f32x4 mk, o;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const bool keep = dropout_u(n + j, m, e.seed + m * 7u) >= e.p;
-                    mk[j] = keep ? scale : 0.0f;
-                    o[j] = keep ? a[j] * scale : 0.0f;
-                }
-                store4<T>(e.mask, idx, mk);
-                store4<T>(e.out, idx, o);
-            } else {
-                store4<T>(e.out, idx, a);
-            }
+            finish(e, (uint64_t)m * e.ldc + n, m, n, v, column(e, n), Pre{});
             return;
         }
 #pragma unroll
@@ -81,35 +100,58 @@ template <typename T> struct EpiFwdK {
 // ---- hidden error: act' * mask, element-local norm gradient --------------------
 template <typename T> struct EpiHiddenK {
     typedef HiddenEpi Params;
+    __device__ __forceinline__ static uint32_t ldc(const HiddenEpi &e) { return e.ldc; }
+    // norm 1 (RMS) reads prenorm, 2 (LN) / 3 (BN) read centered; rstd is per row
+    // for RMS / LN and per column for BN.
+    struct Col { f32x4 nw, rstd; };
+    struct Pre { f32x4 pd, pa, mk, aux; float rstd; };
+    __device__ __forceinline__ static Col column(const HiddenEpi &e, uint32_t n) {
+        Col c;
+        c.nw = e.norm ? *reinterpret_cast<const f32x4 *>(e.nw + n) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        c.rstd = e.norm == 3 ? load4<T>(e.norm_rstd, n) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        return c;
+    }
+    __device__ __forceinline__ static void load(const HiddenEpi &e, uint64_t idx, uint32_t m, Pre &p) {
+        p.pd = load4<T>(e.predrop, idx);
+        p.pa = load4<T>(e.preact, idx);
+        p.mk = load4<T>(e.mask, idx);
+        if (e.norm) p.aux = load4<T>(e.norm == 1 ? e.prenorm : e.centered, idx);
+        if (e.norm == 1 || e.norm == 2) p.rstd = to_f32(ld_t<T>(e.norm_rstd, m));
+    }
+    __device__ __forceinline__ static void finish(const HiddenEpi &e, uint64_t idx, uint32_t, uint32_t, floatx4 v,
+                                                  const Col &col, const Pre &p) {
+        f32x4 err;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) err[j] = p.mk[j] * activation_derivative(e.act, v[j], p.pd[j], p.pa[j], e.leaky);
+        *reinterpret_cast<f32x4 *>(e.grad + idx) = err;
+        f32x4 dp = err;
+        if (e.norm) {
+            f32x4 dnw, dnb;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float rstd = e.norm == 3 ? col.rstd[j] : p.rstd;
+                const float pv = e.norm == 1 ? p.aux[j] : 0.0f;
+                const float cv = e.norm >= 2 ? p.aux[j] : 0.0f;
+                const NormGrad g = norm_grad(e.norm, err[j], pv, cv, rstd, col.nw[j], e.inv_n, e.inv_m);
+                dp[j] = g.d_prenorm;
+                dnw[j] = g.dnw;
+                dnb[j] = g.dnb;
+            }
+            *reinterpret_cast<f32x4 *>(e.d_norm_w + idx) = dnw;
+            *reinterpret_cast<f32x4 *>(e.d_norm_b + idx) = dnb;
+        }
+        dp = dp * e.loss_scale;
+        *reinterpret_cast<f32x4 *>(e.d_prenorm + idx) = dp;
+        if (e.d_prenorm_h) store4<half_t>(e.d_prenorm_h, idx, dp);
+    }
     __device__ __forceinline__ static void apply(const HiddenEpi &e, const GemmShape &sh, uint32_t m,
                                                  uint32_t n, floatx4 v, uint32_t) {
         if (m >= sh.M) return;
         if (n + 3 < sh.N && (e.ldc & 3u) == 0) {
             const uint64_t idx = (uint64_t)m * e.ldc + n;
-            const f32x4 pd = load4<T>(e.predrop, idx), pa = load4<T>(e.preact, idx), mk = load4<T>(e.mask, idx);
-            f32x4 err;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) err[j] = mk[j] * activation_derivative(e.act, v[j], pd[j], pa[j], e.leaky);
-            *reinterpret_cast<f32x4 *>(e.grad + idx) = err;
-            f32x4 dp = err;
-            if (e.norm) {
-                const f32x4 pv = e.norm == 1 ? load4<T>(e.prenorm, idx) : f32x4{0, 0, 0, 0};
-                const f32x4 cv = e.norm >= 2 ? load4<T>(e.centered, idx) : f32x4{0, 0, 0, 0};
-                f32x4 dnw, dnb;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float rstd = to_f32(ld_t<T>(e.norm_rstd, e.norm == 3 ? n + j : m));
-                    const NormGrad g = norm_grad(e.norm, err[j], pv[j], cv[j], rstd, e.nw[n + j], e.inv_n, e.inv_m);
-                    dp[j] = g.d_prenorm;
-                    dnw[j] = g.dnw;
-                    dnb[j] = g.dnb;
-                }
-                *reinterpret_cast<f32x4 *>(e.d_norm_w + idx) = dnw;
-                *reinterpret_cast<f32x4 *>(e.d_norm_b + idx) = dnb;
-            }
-            dp = dp * e.loss_scale;
-            *reinterpret_cast<f32x4 *>(e.d_prenorm + idx) = dp;
-            if (e.d_prenorm_h) store4<half_t>(e.d_prenorm_h, idx, dp);
+            Pre p;
+            load(e, idx, m, p);
+            finish(e, idx, m, n, v, column(e, n), p);
             return;
         }
 #pragma unroll
@@ -141,6 +183,15 @@ template <typename T> struct EpiHiddenK {
 // ---- plain fp32 store (input gradient; split-K partials) -----------------------
 struct EpiStoreK {
     typedef StoreEpi Params;
+    __device__ __forceinline__ static uint32_t ldc(const StoreEpi &e) { return e.ldc; }
+    struct Col {};
+    struct Pre {};
+    __device__ __forceinline__ static Col column(const StoreEpi &, uint32_t) { return Col{}; }
+    __device__ __forceinline__ static void load(const StoreEpi &, uint64_t, uint32_t, Pre &) {}
+    __device__ __forceinline__ static void finish(const StoreEpi &e, uint64_t idx, uint32_t, uint32_t, floatx4 v,
+                                                  const Col &, const Pre &) {
+        *reinterpret_cast<floatx4 *>(e.out + idx) = v;
+    }
     __device__ __forceinline__ static void apply(const StoreEpi &e, const GemmShape &sh, uint32_t m, uint32_t n,
                                                  floatx4 v, uint32_t split) {
         if (m >= sh.M) return;
@@ -158,36 +209,47 @@ struct EpiStoreK {
 // ---- dW + optimiser on W (fused) -----------------------------------------------
 template <typename T> struct EpiOptK {
     typedef OptEpi Params;
+    __device__ __forceinline__ static uint32_t ldc(const OptEpi &e) { return e.ldc; }
+    struct Col {};
+    struct Pre { floatx4 p, dv, dm; };
+    __device__ __forceinline__ static Col column(const OptEpi &, uint32_t) { return Col{}; }
+    __device__ __forceinline__ static void load(const OptEpi &e, uint64_t idx, uint32_t, Pre &q) {
+        q.p = *reinterpret_cast<const floatx4 *>(e.master + idx);
+        q.dv = *reinterpret_cast<const floatx4 *>(e.dv + idx);
+        q.dm = *reinterpret_cast<const floatx4 *>(e.dm + idx);
+    }
+    __device__ __forceinline__ static void finish(const OptEpi &e, uint64_t idx, uint32_t, uint32_t, floatx4 v,
+                                                  const Col &, const Pre &q) {
+        floatx4 p = q.p, dv = q.dv, dm = q.dm;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float pj = p[j], vj = dv[j], mj = dm[j];
+            optimiser_step(pj, vj, mj, v[j] * kLossScaleInv, e.inv_m, e.lr, e.clamp, e.opt, e.regularisation,
+                           e.regu_coeff, true);
+            p[j] = pj; dv[j] = vj; dm[j] = mj;
+        }
+        *reinterpret_cast<floatx4 *>(e.master + idx) = p;
+        *reinterpret_cast<floatx4 *>(e.dv + idx) = dv;
+        *reinterpret_cast<floatx4 *>(e.dm + idx) = dm;
+        if (e.param) {
+            T t[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) t[j] = from_f32<T>(p[j]);
+            if constexpr (sizeof(T) == 2) {
+                *reinterpret_cast<uint64_t *>(reinterpret_cast<T *>(e.param) + idx) = __builtin_bit_cast(uint64_t, t);
+            } else {
+                *reinterpret_cast<floatx4 *>(reinterpret_cast<T *>(e.param) + idx) = __builtin_bit_cast(floatx4, t);
+            }
+        }
+    }
     __device__ __forceinline__ static void apply(const OptEpi &e, const GemmShape &sh, uint32_t m, uint32_t n,
                                                  floatx4 v, uint32_t) {
         if (m >= sh.M) return;
         const uint64_t base = (uint64_t)m * e.ldc;
         if (n + 3 < sh.N && (e.ldc & 3u) == 0) {
-            floatx4 p = *reinterpret_cast<const floatx4 *>(e.master + base + n);
-            floatx4 dv = *reinterpret_cast<const floatx4 *>(e.dv + base + n);
-            floatx4 dm = *reinterpret_cast<const floatx4 *>(e.dm + base + n);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                float pj = p[j], vj = dv[j], mj = dm[j];
-                optimiser_step(pj, vj, mj, v[j] * kLossScaleInv, e.inv_m, e.lr, e.clamp, e.opt, e.regularisation,
-                               e.regu_coeff, true);
-                p[j] = pj; dv[j] = vj; dm[j] = mj;
-            }
-            *reinterpret_cast<floatx4 *>(e.master + base + n) = p;
-            *reinterpret_cast<floatx4 *>(e.dv + base + n) = dv;
-            *reinterpret_cast<floatx4 *>(e.dm + base + n) = dm;
-            if (e.param) {
-                T t[4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) t[j] = from_f32<T>(p[j]);
-                if constexpr (sizeof(T) == 2) {
-                    *reinterpret_cast<uint64_t *>(reinterpret_cast<T *>(e.param) + base + n) =
-                        __builtin_bit_cast(uint64_t, t);
-                } else {
-                    *reinterpret_cast<floatx4 *>(reinterpret_cast<T *>(e.param) + base + n) =
-                        __builtin_bit_cast(floatx4, t);
-                }
-            }
+            Pre q;
+            load(e, base + n, m, q);
+            finish(e, base + n, m, n, v, Col{}, q);
         } else {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -307,9 +369,9 @@ uint32_t gemm_tiles(uint32_t dtype, uint32_t M, uint32_t N) {
 
 uint32_t gemm_bk(uint32_t dtype) { return dtype == 1 ? 64 : 32; }
 
-// The deep-pipelined DMA kernel: fp16, k-contiguous operands, whole 256x256
-// tiles, K a multiple of 32, 32-bit operand offsets.  SOKLYN_GEMM_DMA=0
-// selects the register-staged kernel instead (A/B comparisons).
+// The direct-to-LDS 4-wave kernel: fp16, k-contiguous operands, whole 256x256
+// tiles, K a multiple of 128 (two k-tiles), 32-bit operand offsets.
+// SOKLYN_GEMM_DMA=0 selects the register-staged kernel instead (A/B comparisons).
 static bool dma_enabled() {
     static bool on = [] {
         const char *e = getenv("SOKLYN_GEMM_DMA");
@@ -320,8 +382,18 @@ static bool dma_enabled() {
 
 static bool dma_ok(const GemmLaunch &g) {
     if (!dma_enabled() || g.dtype != 1 || !g.a_kcontig || !g.b_kcontig) return false;
-    if ((g.M % 256) || (g.N % 256) || (g.K % 64) || g.K == 0 || (g.splits && g.splits != 1)) return false;
+    if ((g.M % 256) || (g.N % 256) || (g.K % 128) || g.K == 0 || (g.splits && g.splits != 1)) return false;
     if (!vec_ok(g, 8)) return false;
+    // the batched epilogue accesses 4 columns at a time without edge checks
+    uint32_t ldc = 0;
+    switch (g.op) {
+    case Op::Fwd: ldc = g.fwd.ldc; break;
+    case Op::Hidden: ldc = g.hid.ldc; break;
+    case Op::InputGrad:
+    case Op::DwPartial: ldc = g.st.ldc; break;
+    case Op::DwOpt: ldc = g.opt.ldc; break;
+    }
+    if (ldc % 4) return false;
     return (uint64_t)g.M * g.lda * 2 < (1ull << 32) && (uint64_t)g.N * g.ldb * 2 < (1ull << 32);
 }
 
@@ -338,7 +410,7 @@ template <class Epi> static hipError_t run_dma(const GemmLaunch &g, const typena
     const dim3 grid(sh.tiles_m * sh.tiles_n);
     const half_t *A = reinterpret_cast<const half_t *>(g.A);
     const half_t *B = reinterpret_cast<const half_t *>(g.B);
-    hipLaunchKernelGGL((gemm_dma_kernel<Epi>), grid, dim3(Dma64::NT), 0, s, sh, A, B, p);
+    hipLaunchKernelGGL((gemm_dma_kernel<Epi>), grid, dim3(Dma256::NT), 0, s, sh, A, B, p);
     return hipGetLastError();
 }
 

@@ -75,3 +75,44 @@ def test_backward_large_tiles(ctx, half, M, K, N):
     for n in ("dv_w", "dv_b"):
         e = normwise(db.get(n), getattr(ob, n))
         assert e <= tol, f"{n}: {e:.3e}"
+
+
+# The 256x256 tiles also carry the fused epilogues with dropout, with the
+# norm prologue of the next kernel, and the hidden-error epilogue (act' x mask
+# and the element-local norm gradient).  Output BIG x BIG, reduction 256.
+@pytest.mark.parametrize("norm,act,p", [(0, abi.ACT_SILU, 0.25), (1, abi.ACT_MISH, 0.1), (2, abi.ACT_LEAKY, 0.0)])
+def test_forward_large_tiles_dropout_norm(ctx, norm, act, p):
+    from tests.test_gpu_parity import check, dev, inputs, make_pair
+    M, K, N = BIG, 256, BIG
+    ob, db = make_pair(ctx, K, N, M, seed=41, half=True, norm=norm, act=act, leaky=0.01, p=p)
+    x = inputs(42, M, K, True)
+    seed = O.scramble_seed(5, 9)
+    ob.forward(x, M, p > 0, seed)
+    db.forward(dev(x, True), M, p > 0, seed)
+    torch.cuda.synchronize()
+    for n in ["preact", "predrop", "out"] + (["prenorm", "centered"] if norm else []):
+        check(n, db.get(n)[:M], getattr(ob, n)[:M], FP16_TOL)
+    if p > 0:
+        assert np.array_equal(db.get("mask")[:M], ob.mask[:M]), "dropout mask differs"
+
+
+@pytest.mark.parametrize("norm,act,p", [(0, abi.ACT_SILU, 0.2), (1, abi.ACT_MISH, 0.0), (2, abi.ACT_TANH, 0.1)])
+def test_hidden_error_large_tiles(ctx, norm, act, p):
+    from tests.test_gpu_parity import check, dev, inputs, make_pair
+    M, K0, N0, N1 = BIG, 256, BIG, 256
+    o0, d0 = make_pair(ctx, K0, N0, M, seed=51, half=True, norm=norm, act=act, leaky=0.01, p=p)
+    o1, d1 = make_pair(ctx, N0, N1, M, seed=52, half=True, act=abi.ACT_IDENTITY)
+    x = inputs(53, M, K0, True)
+    seed = 777
+    o0.forward(x, M, p > 0, seed)
+    d0.forward(dev(x, True), M, p > 0, seed)
+    o1.forward(o0.out, M)
+    d1.forward(d0.out, M)
+    t = (rng(54).random((M, N1)) > 0.5).astype(np.float32)
+    o1.output_error(t, abi.LOSS_BCE, abi.ACT_SIGMOID)
+    d1.output_error(dev(t, True), abi.LOSS_BCE, abi.ACT_SIGMOID)
+    o0.hidden_error(o1, M)
+    d0.hidden_error(d1, M)
+    torch.cuda.synchronize()
+    for n in ["grad", "d_prenorm"] + (["d_norm_w", "d_norm_b"] if norm else []):
+        check(n, d0.get(n)[:M], getattr(o0, n)[:M], FP16_TOL)

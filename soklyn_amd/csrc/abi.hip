@@ -330,7 +330,8 @@ int32_t skl_dense_forward(skl_ctx *ctx, const skl_dense_desc *b, const void *in,
     g.fwd.leaky = b->act == SKL_ACT_LEAKY_RELU ? b->leaky : 0.0f;       // ffn_device.rs:32-35
     g.fwd.p = b->mask_coeff;
     g.fwd.ldc = b->outputs;
-    if (use_transposed_operands(b->dtype, batch, b->outputs, b->inputs, in_cols) && aligned16(in)) {
+    if (!gemm_direct_ok(g) && use_transposed_operands(b->dtype, batch, b->outputs, b->inputs, in_cols) &&
+        aligned16(in)) {
         // W^T [N x K] once per call, then the k-contiguous GEMM layout
         const size_t wt_bytes = (size_t)b->inputs * b->outputs * sizeof(uint16_t);
         if ((r = ensure_ws(ctx, wt_bytes))) return r;
@@ -542,19 +543,6 @@ static int32_t backward_impl(skl_ctx *ctx, const skl_dense_desc *b, const void *
     // column partial sums for db / dNorm sums share the workspace
     const uint32_t csplits = colsum_splits(batch, N);
 
-    const bool transposed = splits == 1 && use_transposed_operands(b->dtype, K, N, batch, in_cols) &&
-                            aligned16(in) && aligned16(b->d_prenorm_h);
-    const size_t dw_bytes = splits > 1 ? (size_t)splits * K * N * sizeof(float) : 0;
-    const size_t col_bytes = (size_t)csplits * 3 * N * sizeof(float);
-    const size_t xt_bytes = transposed ? (size_t)K * batch * sizeof(uint16_t) : 0;
-    const size_t pt_bytes = transposed ? (size_t)N * batch * sizeof(uint16_t) : 0;
-    if ((r = ensure_ws(ctx, dw_bytes + col_bytes + xt_bytes + pt_bytes))) return r;
-    char *ws = reinterpret_cast<char *>(ctx->ws);
-    float *ws_dw = reinterpret_cast<float *>(ws);
-    float *ws_col = reinterpret_cast<float *>(ws + dw_bytes);
-    void *ws_xt = ws + dw_bytes + col_bytes;
-    void *ws_pt = ws + dw_bytes + col_bytes + xt_bytes;
-
     GemmLaunch g{};
     g.dtype = b->dtype;
     g.M = K;
@@ -567,6 +555,23 @@ static int32_t backward_impl(skl_ctx *ctx, const skl_dense_desc *b, const void *
     g.A = in;
     g.B = f16 ? b->d_prenorm_h : b->d_prenorm;
     g.splits = splits;
+    g.op = splits == 1 ? Op::DwOpt : Op::DwPartial;
+    g.opt.ldc = N;
+    g.st.ldc = N;
+    const bool transposed = splits == 1 && !gemm_direct_ok(g) &&
+                            use_transposed_operands(b->dtype, K, N, batch, in_cols) && aligned16(in) &&
+                            aligned16(b->d_prenorm_h);
+    const size_t dw_bytes = splits > 1 ? (size_t)splits * K * N * sizeof(float) : 0;
+    const size_t col_bytes = (size_t)csplits * 3 * N * sizeof(float);
+    const size_t xt_bytes = transposed ? (size_t)K * batch * sizeof(uint16_t) : 0;
+    const size_t pt_bytes = transposed ? (size_t)N * batch * sizeof(uint16_t) : 0;
+    if ((r = ensure_ws(ctx, dw_bytes + col_bytes + xt_bytes + pt_bytes))) return r;
+    char *ws = reinterpret_cast<char *>(ctx->ws);
+    float *ws_dw = reinterpret_cast<float *>(ws);
+    float *ws_col = reinterpret_cast<float *>(ws + dw_bytes);
+    void *ws_xt = ws + dw_bytes + col_bytes;
+    void *ws_pt = ws + dw_bytes + col_bytes + xt_bytes;
+
     if (transposed) {
         // X^T [K x batch] and dP^T [N x batch]: both operands k-contiguous
         SKL_TRY(launch_transpose_h(in, ws_xt, batch, K, in_cols, batch, ctx->stream));

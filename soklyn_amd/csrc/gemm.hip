@@ -369,8 +369,8 @@ uint32_t gemm_tiles(uint32_t dtype, uint32_t M, uint32_t N) {
 
 uint32_t gemm_bk(uint32_t dtype) { return dtype == 1 ? 64 : 32; }
 
-// The direct-to-LDS 4-wave kernel: fp16, k-contiguous operands, whole 256x256
-// tiles, K a multiple of 128 (two k-tiles), 32-bit operand offsets.
+// The direct-to-LDS 4-wave kernel: fp16, whole 256x256 tiles, K a multiple of
+// 128 (two k-tiles), 32-bit operand offsets.
 // SOKLYN_GEMM_DMA=0 selects the register-staged kernel instead (A/B comparisons).
 static bool dma_enabled() {
     static bool on = [] {
@@ -380,8 +380,18 @@ static bool dma_enabled() {
     return on;
 }
 
+// Operand layouts the direct-to-LDS kernel is instantiated for: every op with
+// both operands k-contiguous, the forward on W as stored (n-contiguous), and dW
+// on X and dP as stored (m- and n-contiguous).
+static bool dma_layout_ok(const GemmLaunch &g) {
+    if (g.a_kcontig && g.b_kcontig) return true;
+    if (g.op == Op::Fwd) return g.a_kcontig && !g.b_kcontig;
+    if (g.op == Op::DwOpt || g.op == Op::DwPartial) return !g.a_kcontig && !g.b_kcontig;
+    return false;
+}
+
 static bool dma_ok(const GemmLaunch &g) {
-    if (!dma_enabled() || g.dtype != 1 || !g.a_kcontig || !g.b_kcontig) return false;
+    if (!dma_enabled() || g.dtype != 1 || !dma_layout_ok(g)) return false;
     if ((g.M % 256) || (g.N % 256) || (g.K % 128) || g.K == 0 || (g.splits && g.splits != 1)) return false;
     if (!vec_ok(g, 8)) return false;
     // the batched epilogue accesses 4 columns at a time without edge checks
@@ -394,10 +404,15 @@ static bool dma_ok(const GemmLaunch &g) {
     case Op::DwOpt: ldc = g.opt.ldc; break;
     }
     if (ldc % 4) return false;
-    return (uint64_t)g.M * g.lda * 2 < (1ull << 32) && (uint64_t)g.N * g.ldb * 2 < (1ull << 32);
+    // 32-bit byte offsets within each operand
+    const uint64_t a_rows = g.a_kcontig ? g.M : g.K, b_rows = g.b_kcontig ? g.N : g.K;
+    return a_rows * g.lda * 2 < (1ull << 32) && b_rows * g.ldb * 2 < (1ull << 32);
 }
 
-template <class Epi> static hipError_t run_dma(const GemmLaunch &g, const typename Epi::Params &p, hipStream_t s) {
+bool gemm_direct_ok(const GemmLaunch &g) { return gemm_large_tile(g.dtype, g.M, g.N) && dma_ok(g); }
+
+template <class Epi, bool AK, bool BK_>
+static hipError_t run_dma(const GemmLaunch &g, const typename Epi::Params &p, hipStream_t s) {
     GemmShape sh{};
     sh.M = g.M;
     sh.N = g.N;
@@ -410,17 +425,23 @@ template <class Epi> static hipError_t run_dma(const GemmLaunch &g, const typena
     const dim3 grid(sh.tiles_m * sh.tiles_n);
     const half_t *A = reinterpret_cast<const half_t *>(g.A);
     const half_t *B = reinterpret_cast<const half_t *>(g.B);
-    hipLaunchKernelGGL((gemm_dma_kernel<Epi>), grid, dim3(Dma256::NT), 0, s, sh, A, B, p);
+    hipLaunchKernelGGL((gemm_dma_kernel<Epi, AK, BK_>), grid, dim3(Dma256::NT), 0, s, sh, A, B, p);
     return hipGetLastError();
 }
 
 static hipError_t dispatch_dma(const GemmLaunch &g, hipStream_t s) {
+    const bool kk = g.a_kcontig && g.b_kcontig;
     switch (g.op) {
-    case Op::Fwd: return run_dma<EpiFwdK<half_t>>(g, g.fwd, s);
-    case Op::Hidden: return run_dma<EpiHiddenK<half_t>>(g, g.hid, s);
-    case Op::InputGrad:
-    case Op::DwPartial: return run_dma<EpiStoreK>(g, g.st, s);
-    case Op::DwOpt: return run_dma<EpiOptK<half_t>>(g, g.opt, s);
+    case Op::Fwd:
+        return kk ? run_dma<EpiFwdK<half_t>, true, true>(g, g.fwd, s)
+                  : run_dma<EpiFwdK<half_t>, true, false>(g, g.fwd, s);
+    case Op::Hidden: return run_dma<EpiHiddenK<half_t>, true, true>(g, g.hid, s);
+    case Op::InputGrad: return run_dma<EpiStoreK, true, true>(g, g.st, s);
+    case Op::DwPartial:
+        return kk ? run_dma<EpiStoreK, true, true>(g, g.st, s) : run_dma<EpiStoreK, false, false>(g, g.st, s);
+    case Op::DwOpt:
+        return kk ? run_dma<EpiOptK<half_t>, true, true>(g, g.opt, s)
+                  : run_dma<EpiOptK<half_t>, false, false>(g, g.opt, s);
     }
     return hipErrorInvalidValue;
 }

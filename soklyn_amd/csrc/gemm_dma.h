@@ -1,17 +1,17 @@
-// gemm_dma.h — fp16 GEMM for the all-k-contiguous layout on whole 256x256
-// tiles (M % 256 == N % 256 == 0, K % 128 == 0), gfx950.
+// gemm_dma.h — fp16 GEMM on whole 256x256 tiles (M % 256 == N % 256 == 0,
+// K % 128 == 0), gfx950.  Each operand is either k-contiguous in HBM or
+// m/n-contiguous (the forward's W, both operands of dW), so no layout needs a
+// transposed copy.
 //
 //  * 4 waves (1 per SIMD), wave tile 128 x 128 = 4 x 4 v_mfma_f32_32x32x16_f16
 //    blocks; the 256 accumulators live in AGPRs, fragments in VGPRs.  Per
 //    k-step a wave reads 8 x 1 KB fragments from LDS for 16 MFMAs, a third
 //    less LDS read traffic per flop than a 128 x 64 wave tile.
-//  * BK = 64 halves: an LDS row is 128 bytes = 8 chunks of 16 bytes; 2 stages
-//    of 64 KB (A 256 rows + B 256 rows).  Stages are filled by
+//  * BK = 64 halves; 2 stages of 64 KB (A tile + B tile, 32 KB each, laid out
+//    per operand layout as described at OpK / OpN).  Stages are filled by
 //    global_load_lds_dwordx4 (no staging registers, no ds_write): one wave
-//    instruction fills 8 rows x 8 chunks = 1 KB, lane l fetching the global
-//    chunk that belongs in slot l under phys = chunk ^ ((row >> 1) & 7); with
-//    128-byte rows that makes every 16 consecutive rows of a fragment read hit
-//    16 distinct 16-byte bank groups.
+//    instruction fills 1 KB of LDS, each lane fetching the global chunk that
+//    the swizzle puts in its slot.
 //  * Fragments are software-pipelined across the per-tile barrier: the four
 //    k-steps of a tile alternate between two fragment register sets, and the
 //    MFMAs of a tile's last k-step are issued after the barrier, behind the
@@ -42,14 +42,13 @@ namespace skl {
 struct Dma256 {
     static constexpr int BM = 256, BN = 256, BK = 64, WM = 2, WN = 2, NT = 256, NWAVES = 4;
     static constexpr int TWM = BM / WM, TWN = BN / WN, MT = TWM / 32, NTL = TWN / 32;
-    static constexpr int ROWB = BK * 2;            // 128 bytes per LDS row
-    static constexpr int OPB = 256 * ROWB;         // 32 KB per operand tile
+    static constexpr int OPB = 256 * BK * 2;       // 32 KB per operand tile
     static constexpr int STAGEB = 2 * OPB;         // 64 KB per stage
     static constexpr int IPO = OPB / 1024 / NWAVES;   // 8 DMA instructions per operand per wave
-    static constexpr int FRAG_READS = MT + NTL;       // ds_read_b128 per k-step per wave
 };
 
 typedef __attribute__((address_space(3))) char lds_char;
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ void dma16(const char *src, lds_char *dst) {
     __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(src),
@@ -70,21 +69,146 @@ template <int N> __device__ __forceinline__ void wait_lgkmcnt() {
 template <int OFF> __device__ __forceinline__ void ds_read16(u32x4 &dst, uint32_t addr) {
     asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(dst) : "v"(addr), "i"(OFF) : "memory");
 }
-// lgkmcnt(N) that also claims to rewrite the eight fragments it guards, so
-// every MFMA reading them is ordered after the wait by data dependence (a
-// bare s_waitcnt builtin orders memory operations, not the pure MFMAs).
-template <int N> __device__ __forceinline__ void wait_lgkm_frags(u32x4 (&a)[4], u32x4 (&b)[4]) {
-    static_assert(N >= 0 && N < 16, "lgkmcnt range");
+template <int OFF> __device__ __forceinline__ void ds_read8_tr(u32x2 &dst, uint32_t addr) {
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(dst) : "v"(addr), "i"(OFF) : "memory");
+}
+
+// ---- operand staging ------------------------------------------------------------
+// One operand tile of a stage: 256 rows (m or n) x 64 k, 32 KB, filled by 8
+// global_load_lds_dwordx4 per wave (one wave instruction = 1 KB of LDS, lane l
+// writing bytes 16 l .. 16 l + 15), read as four 32-row MFMA fragments of the
+// wave's 128 rows per k-step.  The fragment of a lane holds 8 consecutive k of
+// row l % 32 (k = 8 (l / 32) .. + 7 within the 16-k step).
+//
+// OpK: k-contiguous in HBM (row r at p + r ld).  LDS row = 128 bytes = 8
+// chunks of 8 halves, chunk c of row r stored at slot c ^ ((r >> 1) & 7): any
+// 16 consecutive rows of one chunk column hit 16 distinct 16-byte bank groups.
+// A fragment is one ds_read_b128.
+struct OpK {
+    static constexpr int READS = 4;   // ds_read per k-step
+    struct Frag { u32x4 v[4]; };
+    const char *src;                  // DMA source of this lane, t = 0, k-tile 0
+    uint32_t step;                    // bytes between DMA instructions (32 rows)
+    uint32_t lds;                     // LDS byte address of this lane's fragment row, stage 0
+    uint32_t g;                       // swizzle term of the fragment row
+
+    __device__ __forceinline__ void init(const half_t *p, uint32_t ld, uint32_t mn0, uint32_t wbase,
+                                         uint32_t wave, uint32_t lane, uint32_t lds_op) {
+        // instruction t fills rows 32 t + 8 wave .. + 7; lane -> row + lane / 8, slot lane % 8;
+        // (row >> 1) & 7 does not depend on t
+        const uint32_t row0 = 8u * wave + (lane >> 3);
+        const uint32_t kc = (lane & 7u) ^ ((row0 >> 1) & 7u);
+        src = reinterpret_cast<const char *>(p) + ((size_t)(mn0 + row0) * ld * 2u + kc * 16u);
+        step = 32u * ld * 2u;
+        const uint32_t frow = lane & 31u;
+        g = (lane >> 5) ^ ((frow >> 1) & 7u);
+        lds = lds_op + (wbase + frow) * 128u;
+    }
+    __device__ __forceinline__ void issue(int kt, lds_char *dst) const {
+        const char *s = src + (uint32_t)kt * 128u;
+#pragma unroll
+        for (int t = 0; t < Dma256::IPO; ++t) dma16(s + t * step, dst + t * 4096u);
+    }
+    // logical chunk 2 ks + (lane / 32) of each fragment row
+    __device__ __forceinline__ void read(Frag &f, uint32_t stage_off, int ks) const {
+        const uint32_t a = lds + stage_off + ((2u * ks) ^ g) * 16u;
+        ds_read16<0 * 4096>(f.v[0], a);
+        ds_read16<1 * 4096>(f.v[1], a);
+        ds_read16<2 * 4096>(f.v[2], a);
+        ds_read16<3 * 4096>(f.v[3], a);
+    }
+    __device__ __forceinline__ static u32x4 op(const Frag &f, int i) { return f.v[i]; }
+};
+
+// OpN: m- (or n-) contiguous in HBM (k-row k at p + k ld).  LDS holds the
+// tile k-major: 64 rows of 512 bytes (256 halves), chunk c of k-row r stored
+// at slot c ^ (4 (r & 3)).  A fragment is two ds_read_b64_tr_b16: in each
+// group of 16 lanes, lane s supplies the 8 bytes at k-row 4 h + s / 4 (+ 8 for
+// lanes 32..63), halves 4 (s % 4) .. + 3 of the group's 16 rows, and receives
+// 4 consecutive k of its own row; h = 0, 1 give k 0..3 and 4..7.  The 32 lanes
+// of a half-wave read 4 k-rows x 64 bytes, which the swizzle spreads over the
+// 4 distinct 64-byte bank windows.  Fragment i of the wave sits 32 rows
+// further on: chunk + 4 i, i.e. the lane's address XOR 64 i.
+struct OpN {
+    static constexpr int READS = 8;
+    struct Frag { u32x2 v[4][2]; };
+    const char *src;
+    uint32_t step;                    // 8 k-rows per DMA instruction of a wave
+    uint32_t kstep;                   // bytes per k-tile (64 k-rows)
+    uint32_t lds[4];                  // per fragment i, stage 0, k-step 0, h = 0
+
+    __device__ __forceinline__ void init(const half_t *p, uint32_t ld, uint32_t mn0, uint32_t wbase,
+                                         uint32_t wave, uint32_t lane, uint32_t lds_op) {
+        // instruction t (q = wave + 4 t) fills k-rows 2 q, 2 q + 1; lane -> k-row 2 q + lane / 32,
+        // slot lane % 32; the swizzle term (k-row & 3) does not depend on t
+        const uint32_t r0 = 2u * wave + (lane >> 5);
+        const uint32_t cl = (lane & 31u) ^ (4u * (r0 & 3u));
+        src = reinterpret_cast<const char *>(p) + ((size_t)r0 * ld * 2u + mn0 * 2u + cl * 16u);
+        step = 8u * ld * 2u;
+        kstep = 64u * ld * 2u;
+        const uint32_t grp = lane >> 4, s = lane & 15u;
+        const uint32_t row = 8u * (grp >> 1) + (s >> 2);
+        const uint32_t col = wbase + 16u * (grp & 1u) + 4u * (s & 3u);   // wbase % 128 == 0
+        const uint32_t rel = row * 512u + (((col >> 3) ^ (4u * (row & 3u))) * 16u) + (col & 7u) * 2u;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) lds[i] = lds_op + (rel ^ (64u * i));
+    }
+    __device__ __forceinline__ void issue(int kt, lds_char *dst) const {
+        const char *s = src + (uint32_t)kt * kstep;
+#pragma unroll
+        for (int t = 0; t < Dma256::IPO; ++t) dma16(s + t * step, dst + t * 4096u);
+    }
+    // k-rows 16 ks + 4 h (+ 8): offsets 8192 ks + 2048 h keep the swizzle (multiples of 4 rows)
+    __device__ __forceinline__ void read(Frag &f, uint32_t stage_off, int ks) const {
+#define SKL_TR2(I)                                                              \
+        ds_read8_tr<0>(f.v[I][0], lds[I] + stage_off + 8192u * ks);            \
+        ds_read8_tr<2048>(f.v[I][1], lds[I] + stage_off + 8192u * ks);
+        SKL_TR2(0) SKL_TR2(1) SKL_TR2(2) SKL_TR2(3)
+#undef SKL_TR2
+    }
+    __device__ __forceinline__ static u32x4 op(const Frag &f, int i) {
+        return u32x4{f.v[i][0].x, f.v[i][0].y, f.v[i][1].x, f.v[i][1].y};
+    }
+};
+
+// lgkmcnt(N) that also claims to rewrite the fragments it guards, so every
+// MFMA reading them is ordered after the wait by data dependence (a bare
+// s_waitcnt builtin orders memory operations, not the pure MFMAs).
+template <int N> __device__ __forceinline__ void wait_frags(OpK::Frag &a, OpK::Frag &b) {
     asm volatile("s_waitcnt lgkmcnt(%8)"
-                 : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3])
+                 : "+v"(a.v[0]), "+v"(a.v[1]), "+v"(a.v[2]), "+v"(a.v[3]), "+v"(b.v[0]), "+v"(b.v[1]),
+                   "+v"(b.v[2]), "+v"(b.v[3])
+                 : "i"(N));
+}
+template <int N> __device__ __forceinline__ void wait_frags(OpK::Frag &a, OpN::Frag &b) {
+    asm volatile("s_waitcnt lgkmcnt(%12)"
+                 : "+v"(a.v[0]), "+v"(a.v[1]), "+v"(a.v[2]), "+v"(a.v[3]), "+v"(b.v[0][0]), "+v"(b.v[0][1]),
+                   "+v"(b.v[1][0]), "+v"(b.v[1][1]), "+v"(b.v[2][0]), "+v"(b.v[2][1]), "+v"(b.v[3][0]),
+                   "+v"(b.v[3][1])
+                 : "i"(N));
+}
+template <int N> __device__ __forceinline__ void wait_frags(OpN::Frag &a, OpN::Frag &b) {
+    asm volatile("s_waitcnt lgkmcnt(%16)"
+                 : "+v"(a.v[0][0]), "+v"(a.v[0][1]), "+v"(a.v[1][0]), "+v"(a.v[1][1]), "+v"(a.v[2][0]),
+                   "+v"(a.v[2][1]), "+v"(a.v[3][0]), "+v"(a.v[3][1]), "+v"(b.v[0][0]), "+v"(b.v[0][1]),
+                   "+v"(b.v[1][0]), "+v"(b.v[1][1]), "+v"(b.v[2][0]), "+v"(b.v[2][1]), "+v"(b.v[3][0]),
+                   "+v"(b.v[3][1])
                  : "i"(N));
 }
 
-template <class Epi>
+template <bool KC> struct DmaOpSel { typedef OpK type; };
+template <> struct DmaOpSel<false> { typedef OpN type; };
+
+template <class Epi, bool A_KC, bool B_KC>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
     gemm_dma_kernel(GemmShape sh, const half_t *__restrict__ A, const half_t *__restrict__ B,
                     typename Epi::Params ep) {
     typedef Dma256 C;
+    typedef typename DmaOpSel<A_KC>::type OA;
+    typedef typename DmaOpSel<B_KC>::type OB;
+    // a fragment set may be consumed while at most the other set's reads are pending
+    constexpr int SET_READS = OA::READS + OB::READS;
+    constexpr int WAIT_SET = SET_READS < 15 ? SET_READS : 15;
     constexpr int EPITCH = C::BN + 4;
     constexpr int MTP = 2;                                   // accumulator rows per epilogue pass
     constexpr int PROWS = C::WM * MTP * 32;
@@ -105,22 +229,16 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
     const uint32_t m0 = tm * C::BM, n0 = tn * C::BN;
     const int nk = (int)(sh.K / C::BK);
 
-    // DMA instruction t of this wave (per operand) fills LDS rows
-    // 32 t + 8 wave .. +7; lane l takes row 32 t + 8 wave + l / 8 and slot
-    // l % 8.  The swizzle term (row >> 1) & 7 does not depend on t.
-    const uint32_t row0 = 8u * wave + (lane >> 3);
-    const uint32_t kc = (lane & 7u) ^ ((row0 >> 1) & 7u);
-    const char *Ab = reinterpret_cast<const char *>(A) + ((size_t)(m0 + row0) * sh.lda * 2u + kc * 16u);
-    const char *Bb = reinterpret_cast<const char *>(B) + ((size_t)(n0 + row0) * sh.ldb * 2u + kc * 16u);
-    const uint32_t astep = 32u * sh.lda * 2u, bstep = 32u * sh.ldb * 2u;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)lsm;   // LDS byte address of smem
+    OA oa;
+    OB ob;
+    oa.init(A, sh.lda, m0, wm * C::TWM, wave, lane, lds0);
+    ob.init(B, sh.ldb, n0, wn * C::TWN, wave, lane, lds0 + C::OPB);
 
     auto issue = [&](int kt, int stage) {
-        const uint32_t kb = (uint32_t)kt * C::BK * 2u;
         lds_char *st = lsm + stage * C::STAGEB + wave * 1024u;
-#pragma unroll
-        for (int t = 0; t < C::IPO; ++t) dma16(Ab + kb + t * astep, st + t * 4096u);
-#pragma unroll
-        for (int t = 0; t < C::IPO; ++t) dma16(Bb + kb + t * bstep, st + C::OPB + t * 4096u);
+        oa.issue(kt, st);
+        ob.issue(kt, st + C::OPB);
     };
 
     floatx16 acc[C::MT][C::NTL];
@@ -131,34 +249,19 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    // Fragment byte offsets in a stage: row part + swizzled chunk for k-step ks:
-    // phys = (2 ks + fhalf) ^ ((row >> 1) & 7) = 2 ks ^ g with g = fhalf ^ ((frow >> 1) & 7)
-    // (tile and wave row bases are multiples of 32, so they do not change the swizzle).
-    const uint32_t g = fhalf ^ ((frow >> 1) & 7u);
-    const uint32_t lds0 = (uint32_t)(uintptr_t)lsm;   // LDS byte address of smem
-    const uint32_t a_row = lds0 + (wm * C::TWM + frow) * C::ROWB;
-    const uint32_t b_row = lds0 + C::OPB + (wn * C::TWN + frow) * C::ROWB;
-
-    u32x4 fa[2][C::MT], fb[2][C::NTL];
+    typename OA::Frag fa[2];
+    typename OB::Frag fb[2];
     auto read = [&](int set, int stage, int ks) {
-        const uint32_t c = stage * C::STAGEB + ((2u * ks) ^ g) * 16u;
-        ds_read16<0 * 32 * C::ROWB>(fa[set][0], a_row + c);
-        ds_read16<1 * 32 * C::ROWB>(fa[set][1], a_row + c);
-        ds_read16<2 * 32 * C::ROWB>(fa[set][2], a_row + c);
-        ds_read16<3 * 32 * C::ROWB>(fa[set][3], a_row + c);
-        ds_read16<0 * 32 * C::ROWB>(fb[set][0], b_row + c);
-        ds_read16<1 * 32 * C::ROWB>(fb[set][1], b_row + c);
-        ds_read16<2 * 32 * C::ROWB>(fb[set][2], b_row + c);
-        ds_read16<3 * 32 * C::ROWB>(fb[set][3], b_row + c);
+        oa.read(fa[set], stage * C::STAGEB, ks);
+        ob.read(fb[set], stage * C::STAGEB, ks);
     };
-    static_assert(C::MT == 4 && C::NTL == 4, "read() is written out for a 4 x 4 wave tile");
+    static_assert(C::MT == 4 && C::NTL == 4, "operand reads are written out for 4 x 4 fragments");
     auto mma = [&](int set) {
-        // This set landed; the other set's 8 reads may still be in flight.
-        wait_lgkm_frags<C::FRAG_READS>(fa[set], fb[set]);
+        wait_frags<WAIT_SET>(fa[set], fb[set]);
 #pragma unroll
         for (int i = 0; i < C::MT; ++i)
 #pragma unroll
-            for (int j = 0; j < C::NTL; ++j) Mfma<half_t>::run(acc[i][j], fb[set][j], fa[set][i]);
+            for (int j = 0; j < C::NTL; ++j) Mfma<half_t>::run(acc[i][j], OB::op(fb[set], j), OA::op(fa[set], i));
     };
 
     // prologue: tile 0 resident, tile 1 in flight, first fragments read

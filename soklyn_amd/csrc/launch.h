@@ -72,6 +72,9 @@ hipError_t launch_gemm(const GemmLaunch &g, hipStream_t stream);
 uint32_t gemm_tiles(uint32_t dtype, uint32_t M, uint32_t N);
 // True when an fp16 GEMM of this output size uses the 256x256 tile (k-contiguous operands only).
 bool gemm_large_tile(uint32_t dtype, uint32_t M, uint32_t N);
+// True when this launch runs on the 256x256 direct-to-LDS kernel with its operand
+// layouts as given (then transposed operand copies buy nothing).
+bool gemm_direct_ok(const GemmLaunch &g);
 uint32_t gemm_bk(uint32_t dtype);
 
 // ---- element-wise / row / column kernels -------------------------------------

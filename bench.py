@@ -1,6 +1,7 @@
 """Headline benchmark: fp16 DenseBlock fwd+bwd+Adam at B=8192, 4096->4096 on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3|c2] [--no-cpu]
+    python bench.py --copy-probe MIB      (counter calibration copy only)
 
 One step = one pass of the DenseBlock hot path over one batch, all through the
 C ABI (libsoklyn_hip.so), inputs resident in HBM:
@@ -41,11 +42,40 @@ def parse():
     p.add_argument("--config", default="c3", choices=sorted(CONFIGS))
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-rows", type=int, default=0, help="rows of the CPU baseline sample (0 = auto)")
+    p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                   help="only run a plain device-to-device copy of MIB MiB (counter calibration) and exit")
     return p.parse_args()
 
 
-def cpu_baseline(cfg, rows: int):
-    """The oracle (C restatement, fp32, OpenMP) on a bounded sample of the same step."""
+def copy_probe(mib: int) -> None:
+    """A plain copy kernel of known size: HBM counters (FETCH_SIZE / WRITE_SIZE) read
+    against it give the bytes-per-count factor used for roofline.traffic."""
+    import torch
+    n = mib << 20
+    a = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes": n, "launches": 3}), flush=True)
+
+
+def traffic_record(config: str, kernel: str):
+    """HBM bytes per launch of the roofline kernel, from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE and WRITE_SIZE passes, each scaled by the copy-probe factor)."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f).get(config, {}).get(kernel)
+    except (OSError, ValueError):
+        return None
+    return rec
+
+
+def cpu_baseline(cfg, rows: int, reps: int = 3):
+    """The oracle (C restatement, fp32, OpenMP over the host cores) on the same step:
+    one warm-up pass, then the median of `reps` timed passes."""
     from oracle import oracle as O
     K, N = cfg["K"], cfg["N"]
     g = np.random.default_rng(0)
@@ -54,20 +84,29 @@ def cpu_baseline(cfg, rows: int):
     s = (g.standard_normal((rows, N)) * 512).astype(np.float32)
     ob = O.OracleBlock(K, N, rows, w, act=cfg["act"])
     opt = O.Optimiser.adam() if cfg["half"] else O.Optimiser.sgd()
-    t0 = time.perf_counter()
-    ob.forward(x, rows)
-    ob.error_from_sum(s, rows)
-    ob.backward(x, opt, opt, rows, 1e-3, 3.4e38, 1)
-    ob.input_grad(rows)
-    dt = time.perf_counter() - t0
+
+    def one(step):
+        t0 = time.perf_counter()
+        ob.forward(x, rows)
+        ob.error_from_sum(s, rows)
+        ob.backward(x, opt, opt, rows, 1e-3, 3.4e38, step)
+        ob.input_grad(rows)
+        return time.perf_counter() - t0
+
+    one(1)
+    times = sorted(one(2 + i) for i in range(reps))
+    dt = times[len(times) // 2]
     flops = 3 * 2.0 * rows * K * N
     return {"value": round(flops / dt / 1e12, 6), "unit": "TFLOP/s", "cores": O.num_threads(), "kind": "port",
             "sample": f"{rows} of {cfg['M']} batch rows of the same step (fwd, act', dW+update, dX) in fp32 "
-                      f"on the oracle; {dt:.2f} s"}
+                      f"on the oracle; median of {reps} passes after one warm-up, {dt:.2f} s per pass"}
 
 
 def main():
     args = parse()
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
               "multi-GPU sharding is a design note, not a measured path", file=sys.stderr)
@@ -97,56 +136,49 @@ def main():
     tc = abi.train_ctx(opt, opt, M, 1e-3 if half else 1e-2)
     step_no = [0]
 
-    def step():
+    calls = ("forward_gemm", "error_elementwise", "dw_gemm_adam", "dx_gemm")
+
+    def step(ev=None):
+        # ev: per-call (start, end) HIP events on the launch stream, recorded
+        # inside the timed steps so each call is timed in the step's own context
         step_no[0] += 1
-        blk.forward(x, M)
-        blk.error_from_sum(dy, M)
-        blk.backward(x, tc, step_no[0])
-        blk.input_grad(M, dx)
+        fns = (lambda: blk.forward(x, M), lambda: blk.error_from_sum(dy, M),
+               lambda: blk.backward(x, tc, step_no[0]), lambda: blk.input_grad(M, dx))
+        for i, fn in enumerate(fns):
+            if ev is not None:
+                ev[i][0].record(stream)
+            fn()
+            if ev is not None:
+                ev[i][1].record(stream)
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in calls]
+           for _ in range(args.steps)]
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     ev0.record(stream)
-    for _ in range(args.steps):
-        step()
+    for k in range(args.steps):
+        step(evs[k])
     ev1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms = ev0.elapsed_time(ev1) / args.steps
     flops = 3 * 2.0 * M * K * N
     value = flops / (ms * 1e-3) / 1e12
+    # average duration of each call over the timed steps (forward and dX are one
+    # kernel launch each at these shapes; dW+Adam adds the bias column sums)
+    kern = {c: sum(evs[k][i][0].elapsed_time(evs[k][i][1]) for k in range(args.steps)) / args.steps
+            for i, c in enumerate(calls)}
 
-    # Per-kernel live timing (HIP events on the launch stream) of the three GEMMs.
-    reps = max(5, min(20, args.steps))
-
-    def timed(fn):
-        fn()
-        torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(stream)
-        for _ in range(reps):
-            fn()
-        b.record(stream)
-        torch.cuda.synchronize()
-        return a.elapsed_time(b) / reps
-
-    def bwd():
-        step_no[0] += 1
-        blk.backward(x, tc, step_no[0])
-
-    kern = {
-        "forward_gemm": timed(lambda: blk.forward(x, M)),
-        "dx_gemm": timed(lambda: blk.input_grad(M, dx)),
-        "dw_gemm_adam": timed(bwd),
-        "error_elementwise": timed(lambda: blk.error_from_sum(dy, M)),
-    }
+    # The roofline kernel: the slower of the two single-launch GEMM calls (forward:
+    # Z = X.W with the fused bias + activation epilogue; dX = dP.W^T).
     dom = max(("forward_gemm", "dx_gemm"), key=lambda k: kern[k])
     gemm_flops = 2.0 * M * K * N
     achieved = gemm_flops / (kern[dom] * 1e-3) / 1e12
     peak = PEAK["f16" if half else "f32"]
+    trec = traffic_record(args.config, dom)
 
     out = {
         "metric": "DenseBlock fwd+bwd TFLOP/s & % MFMA peak (fp16, B=8192, 4096→4096)",
@@ -164,11 +196,14 @@ def main():
         "config": {"workload": cfg["workload"], "M": M, "K": K, "N": N,
                    "pct_of_peak_step": round(100 * value / peak, 2), "wall_s": round(wall, 3)},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": peak, "unit": "TFLOP/s",
-                     "frac": round(achieved / peak, 4), "traffic": None, "kernel": dom,
+                     "frac": round(achieved / peak, 4),
+                     "traffic": trec["bytes_per_launch"] if trec else None,
+                     "traffic_source": trec["source"] if trec else None, "kernel": dom,
                      "kernel_ms": {k: round(v, 4) for k, v in kern.items()}},
     }
     if not args.no_cpu:
-        rows = args.cpu_rows or (64 if half else 256)
+        # the whole batch: about 10-20 s of the oracle on the host cores
+        rows = args.cpu_rows or M
         out["cpu_baseline"] = cpu_baseline(cfg, rows)
     print(json.dumps(out), flush=True)
     ctx.close()

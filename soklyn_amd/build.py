@@ -1,9 +1,10 @@
-"""Build libsoklyn_hip.so (gfx950) in-tree with hipcc.
+"""Build libsoklyn_hip.so (gfx950) in-tree with hipcc, then the C++ host API
+(soklyn_amd/host: libsoklyn_host.so and the soklyn_tool driver) with g++.
 
     python -m soklyn_amd.build          # or soklyn_amd.build.build()
 
-Objects go to soklyn_amd/_build/, the shared library to
-soklyn_amd/libsoklyn_hip.so (both git-ignored; the .so travels with the tree).
+Objects go to soklyn_amd/_build/, the shared libraries and the tool next to
+their sources (all git-ignored; they travel with the tree).
 """
 from __future__ import annotations
 
@@ -17,6 +18,12 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libsoklyn_hip.so")
+HOST = os.path.join(HERE, "host")
+INCLUDE = os.path.join(os.path.dirname(HERE), "include")
+HOST_LIB = os.path.join(HOST, "libsoklyn_host.so")
+HOST_TOOL = os.path.join(HOST, "soklyn_tool")
+# the host API restates f32 expressions in the reference's evaluation order: no contraction
+GXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Wall", "-Wextra", "-I", INCLUDE, "-I", HOST]
 SOURCES = ["gemm.hip", "elementwise.hip", "abi.hip"]
 ARCH = os.environ.get("SOKLYN_OFFLOAD_ARCH", "gfx950")
 
@@ -57,9 +64,29 @@ def build(verbose: bool = True) -> str:
     if p.returncode != 0:
         raise RuntimeError("link failed:\n" + p.stdout + p.stderr)
     os.replace(tmp, LIB)
+    build_host()
     if verbose:
-        print(f"[soklyn_amd] built {LIB}", flush=True)
+        print(f"[soklyn_amd] built {LIB}, {HOST_LIB}, {HOST_TOOL}", flush=True)
     return LIB
+
+
+def _run(cmd, what):
+    p = subprocess.run(cmd, capture_output=True, text=True)
+    if p.returncode != 0:
+        raise RuntimeError(f"{what} failed:\n{p.stdout}{p.stderr}")
+
+
+def build_host() -> None:
+    """libsoklyn_host.so (the C++ host API over the C ABI) and soklyn_tool."""
+    gxx = shutil.which("g++") or "g++"
+    rocm_lib = "/opt/rocm/lib"
+    _run([gxx, *GXX_FLAGS, "-shared", os.path.join(HOST, "soklyn.cpp"), "-L", HERE, "-lsoklyn_hip",
+          "-Wl,-rpath,$ORIGIN/..", f"-Wl,-rpath-link,{rocm_lib}", "-o", HOST_LIB + ".tmp"], "host library")
+    os.replace(HOST_LIB + ".tmp", HOST_LIB)
+    _run([gxx, *GXX_FLAGS, os.path.join(HOST, "soklyn_tool.cpp"), "-L", HOST, "-lsoklyn_host", "-L", HERE,
+          "-lsoklyn_hip", "-Wl,-rpath,$ORIGIN", "-Wl,-rpath,$ORIGIN/..", f"-Wl,-rpath-link,{rocm_lib}",
+          "-o", HOST_TOOL + ".tmp"], "host tool")
+    os.replace(HOST_TOOL + ".tmp", HOST_TOOL)
 
 
 if __name__ == "__main__":

@@ -1,0 +1,299 @@
+// soklyn_tool — command-line driver of the C++ host API (soklyn.hpp).
+//
+//   soklyn_tool selftest                      host-only checks (no GPU needed)
+//   soklyn_tool chacha ROUNDS KEYHEX COUNTER NBLOCKS
+//                                             ChaCha keystream words (hex), 64-bit counter
+//   soklyn_tool pcg32 SEED SEQ N              pcg-c's pcg32 sequence (hex)
+//   soklyn_tool init KIND SEED FACTOR FAN_IN FAN_OUT LEN
+//                                             initialiser output as f32 bit patterns (hex);
+//                                             KIND = he_normal | he_uniform | xavier_normal |
+//                                             xavier_uniform
+//   soklyn_tool ids                           tensor ids taken by fp32 / fp16 training and
+//                                             inference blocks (needs a GPU)
+//   soklyn_tool train DIR                     FeedForwardNetwork training steps described by
+//                                             DIR/spec.txt on DIR/x.bin, DIR/t.bin (needs a GPU)
+//
+// `train` writes, per layer i: w<i>_init.bin (initial weights as f32), and after
+// the last step out<i>, w<i>, master_w<i> (fp16), b<i>, dv_w<i>, dm_w<i>, dv_b<i>,
+// grad<i>, d_prenorm<i>, mask<i> as raw little-endian f32; ids.txt holds each
+// layer's weight tensor id (the dropout seed is scramble_seed(step, id)).
+#include <cfloat>
+#include <cinttypes>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <fstream>
+#include <map>
+#include <memory>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include "soklyn.hpp"
+
+using namespace soklyn;
+
+namespace {
+
+int usage() {
+    std::fprintf(stderr, "usage: soklyn_tool selftest | chacha R KEYHEX CTR N | init KIND SEED FACTOR FIN FOUT LEN | "
+                         "ids | train DIR\n");
+    return 2;
+}
+
+int selftest() {
+    int bad = 0;
+    // every binary16 value survives f16 -> f32 -> f16 (NaNs stay NaN)
+    for (uint32_t b = 0; b < 65536; ++b) {
+        f16 h;
+        h.bits = static_cast<uint16_t>(b);
+        const float f = h.to_f32();
+        const f16 back = f16::from_f32(f);
+        const bool nan = ((b >> 10) & 0x1f) == 0x1f && (b & 0x3ff);
+        if (nan ? !(((back.bits >> 10) & 0x1f) == 0x1f && (back.bits & 0x3ff)) : back.bits != b) {
+            if (bad++ < 5) std::fprintf(stderr, "f16 round trip %04x -> %04x\n", b, back.bits);
+        }
+    }
+    // ties to even at the subnormal and normal boundaries, overflow
+    struct Case { float v; uint16_t bits; } cases[] = {
+        {1.0f, 0x3c00}, {65504.0f, 0x7bff}, {65519.99f, 0x7bff}, {65520.0f, 0x7c00}, {-65520.0f, 0xfc00},
+        {5.9604644775390625e-08f, 0x0001}, {2.98023223876953125e-08f, 0x0000}, {2.9802326e-08f, 0x0001},
+        {8.940696716308594e-08f, 0x0002}, {1.0009765625f, 0x3c01}, {1.00048828125f, 0x3c00},
+        {1.00146484375f, 0x3c02}, {6.097555160522461e-05f, 0x03ff}, {6.103515625e-05f, 0x0400},
+    };
+    for (const Case &c : cases) {
+        const f16 h = f16::from_f32(c.v);
+        if (h.bits != c.bits) {
+            std::fprintf(stderr, "f16::from_f32(%.10g) = %04x, want %04x\n", c.v, h.bits, c.bits);
+            ++bad;
+        }
+    }
+    // status codes map onto the reference's Error variants
+    const std::pair<int32_t, ErrorKind> kinds[] = {
+        {SKL_ERR_INVALID_CONFIGURATION, ErrorKind::InvalidConfiguration},
+        {SKL_ERR_TRAINING_MODE_REQUIRED, ErrorKind::TrainingModeRequired},
+        {SKL_ERR_ALLOCATION_LIMIT, ErrorKind::AllocationLimitExceeded},
+        {SKL_ERR_MISMATCHED_DIMENSIONS, ErrorKind::MismatchedDimensions},
+        {SKL_ERR_INVALID_BATCH_SIZE, ErrorKind::InvalidBatchSize},
+        {SKL_ERR_NO_DEVICE, ErrorKind::NoDevice},
+        {1, ErrorKind::DriverError},
+    };
+    for (const auto &k : kinds) {
+        try {
+            check(k.first, "selftest");
+            ++bad;
+        } catch (const Error &e) {
+            if (e.kind() != k.second || e.status() != k.first) ++bad;
+        }
+    }
+    try {
+        check(SKL_OK, "selftest");
+    } catch (...) {
+        ++bad;
+    }
+    if (scramble_seed(1, 7) != skl_scramble_seed(1, 7)) ++bad;
+    std::printf("%s\n", bad ? "FAIL" : "OK");
+    return bad ? 1 : 0;
+}
+
+int chacha(int rounds, const char *keyhex, uint64_t counter, int nblocks) {
+    uint32_t k[8] = {};
+    if (std::strlen(keyhex) != 64) return usage();
+    for (int i = 0; i < 32; ++i) {
+        unsigned v = 0;
+        std::sscanf(keyhex + 2 * i, "%2x", &v);
+        k[i / 4] |= static_cast<uint32_t>(v) << (8 * (i % 4));
+    }
+    for (int b = 0; b < nblocks; ++b) {
+        uint32_t out[16];
+        ChaCha8Rng::block(k, counter + b, rounds, out);
+        for (int i = 0; i < 16; ++i) std::printf("%08x%c", out[i], i == 15 ? '\n' : ' ');
+    }
+    return 0;
+}
+
+// pcg-c's pcg32_srandom_r / pcg32_random_r sequence (outputs from the state
+// before each step), used to pin the XSH-RR output and the LCG multiplier.
+int pcg32(uint64_t seed, uint64_t seq, int n) {
+    const uint64_t inc = (seq << 1u) | 1u;
+    uint64_t state = 0;
+    state = state * PCG32_MULTIPLIER + inc;
+    state += seed;
+    state = state * PCG32_MULTIPLIER + inc;
+    for (int i = 0; i < n; ++i) {
+        const uint64_t old = state;
+        state = old * PCG32_MULTIPLIER + inc;
+        std::printf("%08x%c", pcg32_xsh_rr(old), i + 1 == n ? '\n' : ' ');
+    }
+    return 0;
+}
+
+int init_dump(const std::string &kind, uint64_t seed, float factor, size_t fan_in, size_t fan_out, size_t len) {
+    std::unique_ptr<InitFunc> f;
+    if (kind == "he_normal") f.reset(new InitHeNormalFunc(seed, factor));
+    else if (kind == "he_uniform") f.reset(new InitHeUniformFunc(seed, factor));
+    else if (kind == "xavier_normal") f.reset(new InitXavierNormalFunc(seed, factor));
+    else if (kind == "xavier_uniform") f.reset(new InitXavierUniformFunc(seed, factor));
+    else return usage();
+    const std::vector<float> v = f->init_f32(fan_in, fan_out, len);
+    for (size_t i = 0; i < v.size(); ++i) {
+        uint32_t x;
+        std::memcpy(&x, &v[i], 4);
+        std::printf("%08x%c", x, (i % 8 == 7 || i + 1 == v.size()) ? '\n' : ' ');
+    }
+    return 0;
+}
+
+template <class T> size_t block_ids(const GpuContext &ctx, bool training) {
+    InitZeroFunc zero;
+    const size_t before = peek_tensor_id_counter();
+    DenseBlock<T> b = DenseBlock<T>::new_with_config(ctx, training, 8, 4, 16, zero, LayerInitConfig{});
+    const size_t after = peek_tensor_id_counter();
+    if (b.get_weights().get_id() != before) return 0;   // the weight is the block's first tensor
+    return after - before;
+}
+
+int ids() {
+    GpuContext ctx;
+    std::printf("f32_train %zu\nf16_train %zu\nf32_infer %zu\nf16_infer %zu\n", block_ids<float>(ctx, true),
+                block_ids<f16>(ctx, true), block_ids<float>(ctx, false), block_ids<f16>(ctx, false));
+    return 0;
+}
+
+// ---- train ----------------------------------------------------------------------------------
+std::map<std::string, std::string> read_spec(const std::string &path) {
+    std::ifstream in(path);
+    if (!in) throw std::runtime_error("cannot read " + path);
+    std::map<std::string, std::string> m;
+    std::string line;
+    while (std::getline(in, line)) {
+        const size_t eq = line.find('=');
+        if (line.empty() || line[0] == '#' || eq == std::string::npos) continue;
+        m[line.substr(0, eq)] = line.substr(eq + 1);
+    }
+    return m;
+}
+
+std::vector<float> read_f32(const std::string &path, size_t n) {
+    std::vector<float> v(n);
+    std::ifstream in(path, std::ios::binary);
+    if (!in.read(reinterpret_cast<char *>(v.data()), static_cast<std::streamsize>(n * 4)))
+        throw std::runtime_error("short read: " + path);
+    return v;
+}
+
+void write_f32(const std::string &path, const std::vector<float> &v) {
+    std::ofstream out(path, std::ios::binary);
+    out.write(reinterpret_cast<const char *>(v.data()), static_cast<std::streamsize>(v.size() * 4));
+}
+
+template <class T, size_t R> std::vector<float> host_f32(const GpuContext &ctx, const Tensor<T, R> &t) {
+    const std::vector<T> v = t.download(ctx);
+    std::vector<float> f(v.size());
+    for (size_t i = 0; i < v.size(); ++i) f[i] = PrecisionType<T>::to_f32(v[i]);
+    return f;
+}
+
+Optimiser parse_opt(const std::map<std::string, std::string> &s) {
+    if (s.at("opt") == "adam")
+        return Optimiser::adam(std::stof(s.at("m")), std::stof(s.at("v")), std::stof(s.at("eps")));
+    return Optimiser::sgd(std::stof(s.at("v")), s.at("nesterov") == "1");
+}
+
+template <class T> int train(const std::string &dir, const std::map<std::string, std::string> &s) {
+    std::vector<size_t> dims;
+    {
+        std::stringstream ss(s.at("dims"));
+        std::string tok;
+        while (std::getline(ss, tok, ',')) dims.push_back(std::stoul(tok));
+    }
+    const size_t batch = std::stoul(s.at("batch")), steps = std::stoul(s.at("steps"));
+    const size_t L = dims.size() - 1;
+    GpuContext ctx;
+
+    LayerInitConfig hidden;
+    hidden.normalisation = static_cast<Normalisation>(std::stoul(s.at("norm")));
+    hidden.activation = {static_cast<Activation::Kind>(std::stoul(s.at("act"))), std::stof(s.at("leaky"))};
+    hidden.mask_coeff = std::stof(s.at("mask_coeff"));
+    LayerInitConfig head;   // output layer: Identity, no norm, no dropout
+    InitHeNormalFunc init(std::stoull(s.at("init_seed")), 1.0f);
+    std::vector<DenseBlock<T>> layers;
+    for (size_t i = 0; i < L; ++i)
+        layers.push_back(DenseBlock<T>::new_with_config(ctx, true, dims[i], dims[i + 1], batch, init,
+                                                        i + 1 < L ? hidden : head));
+    {
+        std::ofstream ids(dir + "/ids.txt");
+        for (size_t i = 0; i < L; ++i) {
+            ids << layers[i].get_weights().get_id() << "\n";
+            write_f32(dir + "/w" + std::to_string(i) + "_init.bin", host_f32(ctx, layers[i].get_weights()));
+        }
+    }
+    FeedForwardNetwork<T> net(std::move(layers), dims[0]);
+
+    auto to_t = [](const std::vector<float> &f) {
+        std::vector<T> v(f.size());
+        for (size_t i = 0; i < f.size(); ++i) v[i] = PrecisionType<T>::from_f32(f[i]);
+        return v;
+    };
+    const Tensor2D<T> x = Tensor2D<T>::from_cpu_vector(ctx, to_t(read_f32(dir + "/x.bin", batch * dims[0])),
+                                                       {batch, dims[0]});
+    const Tensor2D<T> t = Tensor2D<T>::from_cpu_vector(ctx, to_t(read_f32(dir + "/t.bin", batch * dims[L])),
+                                                       {batch, dims[L]});
+    const LossConfig loss{static_cast<LossFunc>(std::stoul(s.at("loss"))),
+                          {static_cast<Activation::Kind>(std::stoul(s.at("loss_act"))), 0.0f}};
+    MultiLayerTrainContext tc{std::vector<Optimiser>(L, parse_opt(s)), std::vector<Optimiser>(L, parse_opt(s)), batch,
+                              std::stof(s.at("lr")), FLT_MAX};
+    const bool dropout = s.at("dropout") == "1";
+    for (size_t step = 1; step <= steps; ++step) {
+        const std::vector<const Tensor2D<T> *> outs = net.forward(ctx, x, batch, dropout, step);
+        net.backward(ctx, outs, t, x, loss, tc, step);
+    }
+    ctx.synchronize();
+    for (size_t i = 0; i < L; ++i) {
+        const DenseBlock<T> &b = net.get_layers()[i];
+        const std::string n = std::to_string(i);
+        write_f32(dir + "/out" + n + ".bin", host_f32(ctx, b.get_outputs()));
+        write_f32(dir + "/w" + n + ".bin", host_f32(ctx, b.get_weights()));
+        if (b.get_master_weights()) write_f32(dir + "/master_w" + n + ".bin", host_f32(ctx, *b.get_master_weights()));
+        write_f32(dir + "/b" + n + ".bin", host_f32(ctx, b.get_biases()));
+        write_f32(dir + "/dv_w" + n + ".bin", host_f32(ctx, b.get_dv_weights()));
+        write_f32(dir + "/dm_w" + n + ".bin", host_f32(ctx, b.get_dm_weights()));
+        write_f32(dir + "/dv_b" + n + ".bin", host_f32(ctx, b.get_dv_biases()));
+        write_f32(dir + "/grad" + n + ".bin", host_f32(ctx, b.get_grads()));
+        write_f32(dir + "/d_prenorm" + n + ".bin", host_f32(ctx, b.get_delta_prenorm_out()));
+        write_f32(dir + "/mask" + n + ".bin", host_f32(ctx, b.get_masks()));
+    }
+    std::printf("trained %zu steps\n", steps);
+    return 0;
+}
+
+}  // namespace
+
+int main(int argc, char **argv) {
+    if (argc < 2) return usage();
+    const std::string cmd = argv[1];
+    try {
+        if (cmd == "selftest") return selftest();
+        if (cmd == "chacha" && argc == 6)
+            return chacha(std::atoi(argv[2]), argv[3], std::strtoull(argv[4], nullptr, 10), std::atoi(argv[5]));
+        if (cmd == "pcg32" && argc == 5)
+            return pcg32(std::strtoull(argv[2], nullptr, 10), std::strtoull(argv[3], nullptr, 10), std::atoi(argv[4]));
+        if (cmd == "init" && argc == 8)
+            return init_dump(argv[2], std::strtoull(argv[3], nullptr, 10), std::strtof(argv[4], nullptr),
+                             std::strtoul(argv[5], nullptr, 10), std::strtoul(argv[6], nullptr, 10),
+                             std::strtoul(argv[7], nullptr, 10));
+        if (cmd == "ids") return ids();
+        if (cmd == "train" && argc == 3) {
+            const auto spec = read_spec(std::string(argv[2]) + "/spec.txt");
+            return spec.at("dtype") == "f16" ? train<f16>(argv[2], spec) : train<float>(argv[2], spec);
+        }
+    } catch (const Error &e) {
+        std::fprintf(stderr, "soklyn error (status %d): %s\n", e.status(), e.what());
+        return 3;
+    } catch (const std::exception &e) {
+        std::fprintf(stderr, "error: %s\n", e.what());
+        return 4;
+    }
+    return usage();
+}

@@ -1,0 +1,119 @@
+"""The C++ host API end to end on the GPU: FeedForwardNetwork training steps driven by
+soklyn_tool (DenseBlock::new_with_config with InitHeNormalFunc, forward with dropout
+seeded by scramble_seed(step, weight id), compute_loss, backward_output and
+backward_hidden in the order of src/ffn.rs:113-166), checked against the oracle run on
+the same initial weights, inputs and seeds; and the tensor-id sequence of
+src/mlp.rs:46-421 (23 ids per fp32 training block, 27 per fp16 one).
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from soklyn_amd import abi
+from tests.helpers import FP16_TOL, FP32_TOL, f16, normwise, rng
+from tests.test_gpu_ffn import oracle_step
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+TOOL = os.path.join(ROOT, "soklyn_amd", "host", "soklyn_tool")
+
+
+def tool(*args) -> str:
+    print("soklyn_tool", *args, flush=True)
+    p = subprocess.run([TOOL, *map(str, args)], capture_output=True, text=True, timeout=110)
+    assert p.returncode == 0, p.stdout + p.stderr
+    return p.stdout
+
+
+def test_tensor_ids_per_block():
+    got = dict(l.split() for l in tool("ids").strip().splitlines())
+    # training: linear 2 + 4 moments, norm 2 + 4, caches 6, grads 4, mask 1 (+ 2 + 2 masters for fp16)
+    assert got == {"f32_train": "23", "f16_train": "27", "f32_infer": "11", "f16_infer": "15"}
+
+
+def run_scenario(tmp, *, dtype, dims, batch, steps, norm, act, leaky, mask_coeff, loss, loss_act, opt, lr,
+                 dropout, init_seed, x, t):
+    spec = dict(dtype=dtype, dims=",".join(map(str, dims)), batch=batch, steps=steps, norm=norm, act=act,
+                leaky=leaky, mask_coeff=mask_coeff, loss=loss, loss_act=loss_act, lr=lr, dropout=int(dropout),
+                init_seed=init_seed, **opt)
+    with open(os.path.join(tmp, "spec.txt"), "w") as fh:
+        fh.write("".join(f"{k}={v}\n" for k, v in spec.items()))
+    x.astype(np.float32).tofile(os.path.join(tmp, "x.bin"))
+    t.astype(np.float32).tofile(os.path.join(tmp, "t.bin"))
+    tool("train", tmp)
+    L = len(dims) - 1
+    ids = [int(l) for l in open(os.path.join(tmp, "ids.txt")).read().split()]
+    w0 = [np.fromfile(os.path.join(tmp, f"w{i}_init.bin"), np.float32).reshape(dims[i], dims[i + 1])
+          for i in range(L)]
+    res = {}
+    for i in range(L):
+        for n in ("out", "w", "master_w", "b", "dv_w", "dm_w", "dv_b", "grad", "d_prenorm", "mask"):
+            path = os.path.join(tmp, f"{n}{i}.bin")
+            if os.path.exists(path):
+                res[(n, i)] = np.fromfile(path, np.float32)
+    return ids, w0, res
+
+
+def oracle_net(dims, batch, half, w0, hidden_kw):
+    obs = []
+    for i in range(len(dims) - 1):
+        kw = dict(hidden_kw) if i < len(dims) - 2 else dict(act=abi.ACT_IDENTITY)
+        obs.append(O.OracleBlock(dims[i], dims[i + 1], batch, w0[i], half=half, master_w=w0[i] if half else None,
+                                 **kw))
+    return obs
+
+
+def compare(obs, res, tol, half, masks):
+    for i, ob in enumerate(obs):
+        for n in ("out", "grad", "d_prenorm", "dv_w", "dm_w", "dv_b", "master_w" if half else "w"):
+            ref = np.asarray(getattr(ob, n), np.float32).reshape(-1)
+            e = normwise(res[(n, i)], ref)
+            assert e <= tol, f"layer {i} {n}: {e:.3e}"
+        if masks and i < len(obs) - 1:
+            assert np.array_equal(res[("mask", i)], np.asarray(ob.mask, np.float32).reshape(-1)), f"layer {i} mask"
+
+
+def test_ffn_fp32_sgd_two_steps(tmp_path):
+    """784 -> 128 (ReLU) -> 10 (softmax CE), fp32, SGD with momentum, two steps (config 1's shape)."""
+    dims, M, steps = [784, 128, 10], 64, 2
+    g = rng(201)
+    x = g.random((M, 784), dtype=np.float32)
+    t = np.zeros((M, 10), np.float32)
+    t[np.arange(M), g.integers(0, 10, M)] = 1
+    ids, w0, res = run_scenario(str(tmp_path), dtype="f32", dims=dims, batch=M, steps=steps, norm=0,
+                                act=abi.ACT_RELU, leaky=0.0, mask_coeff=0.0, loss=abi.LOSS_CE,
+                                loss_act=abi.ACT_SOFTMAX, opt=dict(opt="sgd", v=0.9, nesterov=0), lr=0.01,
+                                dropout=False, init_seed=42, x=x, t=t)
+    # He-normal: sigma = sqrt(2 / fan_in)
+    assert abs(w0[0].std() / np.sqrt(2 / 784) - 1) < 0.05
+    obs = oracle_net(dims, M, False, w0, dict(act=abi.ACT_RELU))
+    for step in range(1, steps + 1):
+        seeds = [O.scramble_seed(step, i) for i in ids]
+        oracle_step(obs, x, t, M, abi.LOSS_CE, abi.ACT_SOFTMAX, O.Optimiser.sgd(0.9), 0.01, step, False, seeds)
+    compare(obs, res, FP32_TOL, False, masks=False)
+
+
+def test_ffn_fp16_rms_mish_dropout_adam_two_steps(tmp_path):
+    """96 -> 64 -> 64 -> 10, RMSNorm + Mish + dropout 0.1 hidden layers, CE, Adam, fp16 (config 4's
+    layer recipe at a small size); the dropout masks must match bit for bit."""
+    dims, M, steps = [96, 64, 64, 10], 256, 2
+    g = rng(202)
+    x = f16(g.random((M, 96), dtype=np.float32))
+    t = np.zeros((M, 10), np.float32)
+    t[np.arange(M), g.integers(0, 10, M)] = 1
+    ids, w0, res = run_scenario(str(tmp_path), dtype="f16", dims=dims, batch=M, steps=steps, norm=abi.NORM_RMS,
+                                act=abi.ACT_MISH, leaky=0.0, mask_coeff=0.1, loss=abi.LOSS_CE,
+                                loss_act=abi.ACT_SOFTMAX, opt=dict(opt="adam", m=0.9, v=0.999, eps=1e-8),
+                                lr=1e-3, dropout=True, init_seed=7, x=x, t=t)
+    assert ids[1] - ids[0] == 27 and ids[2] - ids[1] == 27   # one fp16 training block apart
+    obs = oracle_net(dims, M, True, w0, dict(norm=abi.NORM_RMS, act=abi.ACT_MISH, mask_coeff=0.1))
+    for step in range(1, steps + 1):
+        seeds = [O.scramble_seed(step, i) for i in ids]
+        oracle_step(obs, x, t, M, abi.LOSS_CE, abi.ACT_SOFTMAX, O.Optimiser.adam(), 1e-3, step, True, seeds)
+    compare(obs, res, FP16_TOL, True, masks=True)

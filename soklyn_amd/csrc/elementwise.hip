@@ -278,7 +278,7 @@ template <typename T> __global__ void error_from_sum_kernel(ErrArgs a) {
 // 16-byte aligned buffers): 16-byte fp32 / 8-byte fp16 accesses, 32-bit indexing.
 template <typename T>
 __device__ __forceinline__ void write_err4(const ErrArgs &a, uint64_t idx, uint32_t row, uint32_t col, f32x4 e) {
-    *reinterpret_cast<f32x4 *>(a.grad + idx) = e;
+    __builtin_nontemporal_store(e, reinterpret_cast<f32x4 *>(a.grad + idx));
     f32x4 dp = e;
     if (a.norm) {
         const f32x4 pv = a.norm == 1 ? load4<T>(a.prenorm, idx) : f32x4{0, 0, 0, 0};
@@ -297,7 +297,7 @@ __device__ __forceinline__ void write_err4(const ErrArgs &a, uint64_t idx, uint3
         *reinterpret_cast<f32x4 *>(a.d_norm_b + idx) = dnb;
     }
     dp = dp * a.loss_scale;
-    *reinterpret_cast<f32x4 *>(a.d_prenorm + idx) = dp;
+    __builtin_nontemporal_store(dp, reinterpret_cast<f32x4 *>(a.d_prenorm + idx));
     if (a.d_prenorm_h) store4<half_t>(a.d_prenorm_h, idx, dp);
 }
 
@@ -323,17 +323,35 @@ template <typename T> __global__ void __launch_bounds__(256) output_error_vec_ke
     }
 }
 
+// A workgroup owns ERR_U x 256 consecutive 4-element groups; a thread loads all
+// ERR_U of its groups before computing any, so each keeps ERR_U x 40 bytes in flight.
+constexpr int ERR_U = 4;
 template <typename T> __global__ void __launch_bounds__(256) error_from_sum_vec_kernel(ErrArgs a) {
     const uint32_t nv = a.n >> 2, total = a.rows * nv;
-    for (uint32_t q = blockIdx.x * blockDim.x + threadIdx.x; q < total; q += gridDim.x * blockDim.x) {
-        const uint32_t row = q / nv, col = (q - row * nv) << 2;
-        const uint64_t idx = (uint64_t)row * a.n + col;
-        const f32x4 s = *reinterpret_cast<const f32x4 *>(a.s + idx);
-        const f32x4 pd = load4<T>(a.predrop, idx), pa = load4<T>(a.preact, idx), mk = load4<T>(a.mask, idx);
-        f32x4 e;
+    for (uint32_t q0 = blockIdx.x * (ERR_U * 256) + threadIdx.x; q0 < total; q0 += gridDim.x * (ERR_U * 256)) {
+        f32x4 s[ERR_U], pd[ERR_U], pa[ERR_U], mk[ERR_U];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) e[j] = mk[j] * activation_derivative(a.act, s[j], pd[j], pa[j], a.leaky);
-        write_err4<T>(a, idx, row, col, e);
+        for (int u = 0; u < ERR_U; ++u) {
+            const uint32_t q = q0 + u * 256;
+            if (q >= total) break;
+            const uint32_t row = q / nv, col = (q - row * nv) << 2;
+            const uint64_t idx = (uint64_t)row * a.n + col;
+            s[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(a.s + idx));
+            pd[u] = load4<T>(a.predrop, idx);
+            pa[u] = load4<T>(a.preact, idx);
+            mk[u] = load4<T>(a.mask, idx);
+        }
+#pragma unroll
+        for (int u = 0; u < ERR_U; ++u) {
+            const uint32_t q = q0 + u * 256;
+            if (q >= total) break;
+            const uint32_t row = q / nv, col = (q - row * nv) << 2;
+            f32x4 e;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                e[j] = mk[u][j] * activation_derivative(a.act, s[u][j], pd[u][j], pa[u][j], a.leaky);
+            write_err4<T>(a, (uint64_t)row * a.n + col, row, col, e);
+        }
     }
 }
 
@@ -370,10 +388,11 @@ hipError_t launch_error_from_sum(const ErrArgs &a, hipStream_t s) {
     const uint64_t total = (uint64_t)a.rows * a.n;
     if (total == 0) return hipSuccess;
     if (err_vec_ok(a, true)) {
+        const dim3 g = grid_for(total / 4, 256 * ERR_U);
         if (a.dtype == 1)
-            hipLaunchKernelGGL(error_from_sum_vec_kernel<half_t>, grid_for(total / 4, 256), dim3(256), 0, s, a);
+            hipLaunchKernelGGL(error_from_sum_vec_kernel<half_t>, g, dim3(256), 0, s, a);
         else
-            hipLaunchKernelGGL(error_from_sum_vec_kernel<float>, grid_for(total / 4, 256), dim3(256), 0, s, a);
+            hipLaunchKernelGGL(error_from_sum_vec_kernel<float>, g, dim3(256), 0, s, a);
     } else if (a.dtype == 1) {
         hipLaunchKernelGGL(error_from_sum_kernel<half_t>, grid_for(total, 256), dim3(256), 0, s, a);
     } else {
@@ -398,17 +417,17 @@ __global__ void __launch_bounds__(256) colsum_kernel(VecOptArgs a) {
     }
 }
 
-// 64 columns per workgroup, 4 lanes per column: lane j sums the partials of
-// splits j, j+4, ... in order, then the four are added in a fixed order.
+// 16 columns per workgroup, 16 lanes per column: lane j sums the partials of
+// splits j, j+16, ... in order, then the 16 are added in a fixed pairwise order.
 template <typename T> __global__ void __launch_bounds__(256) vec_opt_kernel(VecOptArgs a) {
-    __shared__ float red[3][4][64];
-    const uint32_t cl = threadIdx.x & 63u, j = threadIdx.x >> 6;
-    const uint32_t col = blockIdx.x * 64 + cl;
+    __shared__ float red[3][16][17];
+    const uint32_t cl = threadIdx.x & 15u, j = threadIdx.x >> 4;
+    const uint32_t col = blockIdx.x * 16 + cl;
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
         float s = 0.0f;
         if (a.enabled[k] && col < a.n)
-            for (uint32_t sp = j; sp < a.splits; sp += 4) s += a.partials[((uint64_t)sp * 3 + k) * a.n + col];
+            for (uint32_t sp = j; sp < a.splits; sp += 16) s += a.partials[((uint64_t)sp * 3 + k) * a.n + col];
         red[k][j][cl] = s;
     }
     __syncthreads();
@@ -416,7 +435,10 @@ template <typename T> __global__ void __launch_bounds__(256) vec_opt_kernel(VecO
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
         if (!a.enabled[k]) continue;
-        const float s = (red[k][0][cl] + red[k][1][cl]) + (red[k][2][cl] + red[k][3][cl]);
+        float t[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) t[i] = red[k][2 * i][cl] + red[k][2 * i + 1][cl];
+        const float s = ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
         float p = a.master[k][col], v = a.dv[k][col], mm = a.dm[k][col];
         optimiser_step(p, v, mm, s * kLossScaleInv, a.inv_m, a.lr, a.clamp, a.opt[k], 0, 0.0f, false);
         a.master[k][col] = p;
@@ -427,7 +449,7 @@ template <typename T> __global__ void __launch_bounds__(256) vec_opt_kernel(VecO
 }
 
 // Vector column sums: a thread owns 4 consecutive columns (one 16-byte load per
-// row); the row range of its split is walked 4 rows at a time for loads in flight.
+// row); the row range of its split is walked 8 rows at a time for loads in flight.
 __global__ void __launch_bounds__(256) colsum_vec_kernel(VecOptArgs a) {
     const uint32_t c = (blockIdx.x * 256 + threadIdx.x) * 4;
     if (c >= a.n) return;
@@ -440,15 +462,12 @@ __global__ void __launch_bounds__(256) colsum_vec_kernel(VecOptArgs a) {
         const float *src = a.src[k] + c;
         f32x4 acc = {0, 0, 0, 0};
         uint32_t r = r0;
-        for (; r + 4 <= r1; r += 4) {
-            const f32x4 v0 = *reinterpret_cast<const f32x4 *>(src + (uint64_t)r * a.n);
-            const f32x4 v1 = *reinterpret_cast<const f32x4 *>(src + (uint64_t)(r + 1) * a.n);
-            const f32x4 v2 = *reinterpret_cast<const f32x4 *>(src + (uint64_t)(r + 2) * a.n);
-            const f32x4 v3 = *reinterpret_cast<const f32x4 *>(src + (uint64_t)(r + 3) * a.n);
-            acc += v0;
-            acc += v1;
-            acc += v2;
-            acc += v3;
+        for (; r + 8 <= r1; r += 8) {
+            f32x4 v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = *reinterpret_cast<const f32x4 *>(src + (uint64_t)(r + i) * a.n);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc += v[i];
         }
         for (; r < r1; ++r) acc += *reinterpret_cast<const f32x4 *>(src + (uint64_t)r * a.n);
         *reinterpret_cast<f32x4 *>(a.partials + ((uint64_t)blockIdx.y * 3 + k) * a.n + c) = acc;
@@ -479,9 +498,9 @@ uint32_t colsum_splits(uint32_t rows, uint32_t n) {
 hipError_t launch_vec_opt(const VecOptArgs &a, hipStream_t s) {
     if (a.n == 0) return hipSuccess;
     if (a.dtype == 1)
-        hipLaunchKernelGGL(vec_opt_kernel<half_t>, dim3(cdiv(a.n, 64)), dim3(256), 0, s, a);
+        hipLaunchKernelGGL(vec_opt_kernel<half_t>, dim3(cdiv(a.n, 16)), dim3(256), 0, s, a);
     else
-        hipLaunchKernelGGL(vec_opt_kernel<float>, dim3(cdiv(a.n, 64)), dim3(256), 0, s, a);
+        hipLaunchKernelGGL(vec_opt_kernel<float>, dim3(cdiv(a.n, 16)), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

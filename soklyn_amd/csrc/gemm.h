@@ -53,6 +53,18 @@ struct GemmShape {
     uint32_t tiles_m, tiles_n;
 };
 
+// Workgroup barrier that orders LDS only: wait for this wave's LDS accesses,
+// then s_barrier.  __syncthreads() also waits for every outstanding global
+// access (its release fence), which would stall on the next tile's loads in the
+// k loop and on the epilogue's global stores; neither needs ordering here.  The
+// empty asm statements keep the compiler from moving memory accesses across.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));   // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // LDS chunk index of (row, kc) in a k-contiguous tile.
 template <bool PADDED> struct LdsLayout;
 template <> struct LdsLayout<true> {
@@ -305,7 +317,7 @@ struct MainLoop {
             sa.store(nxt, tid);
             sb.store(nxt + A_CHUNKS, tid);
         }
-        __syncthreads();
+        lds_barrier();
     }
 
     template <bool GUARD>
@@ -319,7 +331,7 @@ struct MainLoop {
         sb.template load<GUARD>(B, sh.ldb, n0, kbeg, sh.N, kend, tid);
         sa.store(smem, tid);
         sb.store(smem + A_CHUNKS, tid);
-        __syncthreads();
+        lds_barrier();
         for (int kt = 0; kt < nk; kt += 2) {
             step<GUARD, 0>(smem, acc, sa, sb, sh, A, B, m0, n0, kbeg, kend, kt, nk, tid, wm, wn, frow, fhalf);
             if (kt + 1 < nk)
@@ -405,7 +417,7 @@ __global__ void __launch_bounds__(WM *WN * 64)
                     *reinterpret_cast<floatx4 *>(E + r * EPITCH + c) = v;
                 }
         }
-        __syncthreads();
+        lds_barrier();
 #pragma unroll 1
         for (uint32_t q = tid; q < (uint32_t)(PROWS * BN / 4); q += NT) {
             const uint32_t r = q / (BN / 4);
@@ -416,7 +428,7 @@ __global__ void __launch_bounds__(WM *WN * 64)
             const floatx4 v = *reinterpret_cast<const floatx4 *>(E + r * EPITCH + c);
             Epi::apply(ep, sh, m, n0 + c, v, blockIdx.z);
         }
-        __syncthreads();
+        if (pass + 1 < MT / MTP) lds_barrier();   // E is rewritten by the next pass
     }
 }
 

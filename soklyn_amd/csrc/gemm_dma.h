@@ -325,7 +325,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
                     *reinterpret_cast<floatx4 *>(E + r * EPITCH + cc) = v;
                 }
         }
-        __syncthreads();
+        lds_barrier();
 #pragma unroll 1
         for (int b = 0; b < ROWS_PER_THREAD; b += EPI_BATCH) {
             typename Epi::Pre pre[EPI_BATCH];
@@ -345,7 +345,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
                 Epi::finish(ep, (uint64_t)mrow[u] * Epi::ldc(ep) + n0 + c, mrow[u], n0 + c, v, col, pre[u]);
             }
         }
-        __syncthreads();
+        if (pass + 1 < C::MT / MTP) lds_barrier();   // E is rewritten by the next pass
     }
 }
 

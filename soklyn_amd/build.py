@@ -80,7 +80,8 @@ def build_host() -> None:
     """libsoklyn_host.so (the C++ host API over the C ABI) and soklyn_tool."""
     gxx = shutil.which("g++") or "g++"
     rocm_lib = "/opt/rocm/lib"
-    _run([gxx, *GXX_FLAGS, "-shared", os.path.join(HOST, "soklyn.cpp"), "-L", HERE, "-lsoklyn_hip",
+    _run([gxx, *GXX_FLAGS, "-shared", os.path.join(HOST, "soklyn.cpp"), os.path.join(HOST, "safetensors.cpp"),
+          "-L", HERE, "-lsoklyn_hip",
           "-Wl,-rpath,$ORIGIN/..", f"-Wl,-rpath-link,{rocm_lib}", "-o", HOST_LIB + ".tmp"], "host library")
     os.replace(HOST_LIB + ".tmp", HOST_LIB)
     _run([gxx, *GXX_FLAGS, os.path.join(HOST, "soklyn_tool.cpp"), "-L", HOST, "-lsoklyn_host", "-L", HERE,

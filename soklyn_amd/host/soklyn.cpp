@@ -26,8 +26,15 @@ ErrorKind error_kind(int32_t status) {
     case SKL_ERR_NULL_POINTER: return ErrorKind::NullPointer;
     case SKL_ERR_UNSUPPORTED_CAST: return ErrorKind::UnsupportedTypeCast;
     case SKL_ERR_NO_DEVICE: return ErrorKind::NoDevice;
-    default: return ErrorKind::DriverError;
+    default: break;
     }
+    if (status <= HOST_STATUS_BASE && status > HOST_STATUS_BASE - 11)
+        return static_cast<ErrorKind>(static_cast<int>(ErrorKind::SerdeJSON) + (HOST_STATUS_BASE - status));
+    return ErrorKind::DriverError;
+}
+
+int32_t host_status(ErrorKind kind) {
+    return HOST_STATUS_BASE - (static_cast<int32_t>(kind) - static_cast<int32_t>(ErrorKind::SerdeJSON));
 }
 
 void check(int32_t status, const char *what) {

@@ -42,7 +42,22 @@ enum class ErrorKind {
     UnsupportedTypeCast,
     NoDevice,
     DriverError,
+    // host-side variants of the checkpoint format (src/util/log.rs; status codes below -100)
+    SerdeJSON,
+    IOError,
+    PersistError,
+    SerializationCasting,
+    UnrecognizedTensorKey,
+    InvalidTensorName,
+    PrecisionMatch,
+    NoLayersFound,
+    MissingLayer,
+    MissingWeights,
+    MissingBiases,
 };
+// Status codes of the host-only error kinds (no C ABI counterpart).
+constexpr int32_t HOST_STATUS_BASE = -100;
+int32_t host_status(ErrorKind kind);
 
 class Error : public std::runtime_error {
   public:

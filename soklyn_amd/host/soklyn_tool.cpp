@@ -11,7 +11,12 @@
 //   soklyn_tool ids                           tensor ids taken by fp32 / fp16 training and
 //                                             inference blocks (needs a GPU)
 //   soklyn_tool train DIR                     FeedForwardNetwork training steps described by
-//                                             DIR/spec.txt on DIR/x.bin, DIR/t.bin (needs a GPU)
+//                                             DIR/spec.txt on DIR/x.bin, DIR/t.bin (needs a GPU);
+//                                             then saves DIR/net.safetensors, loads it back and
+//                                             checks the reloaded network
+//   soklyn_tool st-demo FILE                  write a synthetic safetensors file (no GPU)
+//   soklyn_tool st-dump FILE                  print a safetensors file: metadata, then per tensor
+//                                             name, dtype, shape and the bytes in hex (no GPU)
 //
 // `train` writes, per layer i: w<i>_init.bin (initial weights as f32), and after
 // the last step out<i>, w<i>, master_w<i> (fp16), b<i>, dv_w<i>, dm_w<i>, dv_b<i>,
@@ -24,12 +29,14 @@
 #include <cstdlib>
 #include <cstring>
 #include <fstream>
+#include <algorithm>
 #include <map>
 #include <memory>
 #include <sstream>
 #include <string>
 #include <vector>
 
+#include "safetensors.hpp"
 #include "soklyn.hpp"
 
 using namespace soklyn;
@@ -141,6 +148,57 @@ int init_dump(const std::string &kind, uint64_t seed, float factor, size_t fan_i
         uint32_t x;
         std::memcpy(&x, &v[i], 4);
         std::printf("%08x%c", x, (i % 8 == 7 || i + 1 == v.size()) ? '\n' : ' ');
+    }
+    return 0;
+}
+
+// ---- safetensors ------------------------------------------------------------------------------
+int st_demo(const std::string &path) {
+    SafetensorFile f;
+    SafetensorWriter &w = const_cast<SafetensorWriter &>(f.writer());
+    std::vector<float> a(6);
+    for (int i = 0; i < 6; ++i) a[i] = 0.5f * static_cast<float>(i) - 1.25f;
+    std::vector<uint8_t> ab(a.size() * 4);
+    std::memcpy(ab.data(), a.data(), ab.size());
+    w.pass("layer1.w", {2, 3}, ab, Precision::FP32);
+    std::vector<uint16_t> h = {f16::from_f32(1.5f).bits, f16::from_f32(-2.0f).bits, f16::from_f32(0.1f).bits,
+                               f16::from_f32(65504.0f).bits, f16::from_f32(-0.0f).bits};
+    std::vector<uint8_t> hb(h.size() * 2);
+    std::memcpy(hb.data(), h.data(), hb.size());
+    w.pass("alpha", {5}, hb, Precision::FP16);
+    const float sc = 3.25f;
+    std::vector<uint8_t> sb(4);
+    std::memcpy(sb.data(), &sc, 4);
+    w.pass("scalar", {}, sb, Precision::FP32);
+    w.pass("empty", {0, 3}, {}, Precision::FP32);
+    f.pass_metadata("name", "demo \"quoted\" \\ / \xc3\xa9 \t tab\n line");
+    f.pass_metadata("epoch", "7");
+    f.pass_metadata("name", "demo \"quoted\" \\ / \xc3\xa9 \t tab\n line\x01");   // replaces in place
+    f.save(path);
+    return 0;
+}
+
+int st_dump(const std::string &path) {
+    const SafetensorFile f = SafetensorFile::read(path);
+    std::vector<std::pair<std::string, std::string>> md = f.get_metadata();
+    std::sort(md.begin(), md.end());
+    for (const auto &kv : md) {
+        JsonValue k, v;
+        k.kind = v.kind = JsonValue::Kind::String;
+        k.text = kv.first;
+        v.text = kv.second;
+        std::printf("meta %s %s\n", k.to_compact().c_str(), v.to_compact().c_str());
+    }
+    std::vector<const SafetensorDescriptor *> ds;
+    for (const SafetensorDescriptor &d : f.writer().get_descriptors()) ds.push_back(&d);
+    std::sort(ds.begin(), ds.end(), [](auto *a, auto *b) { return a->name < b->name; });
+    for (const SafetensorDescriptor *d : ds) {
+        std::printf("tensor %s %s", d->name.c_str(), d->precision == Precision::FP32 ? "F32" : "F16");
+        std::printf(" [");
+        for (size_t i = 0; i < d->shape.size(); ++i) std::printf(i ? ",%zu" : "%zu", d->shape[i]);
+        std::printf("] ");
+        for (uint8_t b : d->data) std::printf("%02x", b);
+        std::printf("\n");
     }
     return 0;
 }
@@ -264,6 +322,45 @@ template <class T> int train(const std::string &dir, const std::map<std::string,
         write_f32(dir + "/d_prenorm" + n + ".bin", host_f32(ctx, b.get_delta_prenorm_out()));
         write_f32(dir + "/mask" + n + ".bin", host_f32(ctx, b.get_masks()));
     }
+    // checkpoint round trip (save.rs): save, read back into blocks, compare every
+    // tensor bit for bit, then the reloaded network's forward against the original's
+    {
+        SafetensorFile sf = SafetensorFile::from_ffn(ctx, net);
+        sf.pass_metadata("steps", std::to_string(steps));
+        sf.save(dir + "/net.safetensors");
+        std::vector<DenseBlock<T>> back =
+            SafetensorFile::read(dir + "/net.safetensors").template into_blocks<T>(ctx, true, batch);
+        if (back.size() != L) throw std::runtime_error("round trip: layer count");
+        auto same = [&](const auto &a, const auto &b, const char *what, size_t i) {
+            const auto va = a.download(ctx), vb = b.download(ctx);
+            if (va.size() != vb.size() || std::memcmp(va.data(), vb.data(), va.size() * sizeof(va[0])) != 0)
+                throw std::runtime_error(std::string("round trip: ") + what + " of layer " + std::to_string(i));
+        };
+        for (size_t i = 0; i < L; ++i) {
+            const DenseBlock<T> &o = net.get_layers()[i];
+            DenseBlock<T> &r = back[i];
+            same(o.get_weights(), r.get_weights(), "w", i);
+            same(o.get_biases(), r.get_biases(), "b", i);
+            same(o.get_norm_weights(), r.get_norm_weights(), "norm_w", i);
+            same(o.get_norm_biases(), r.get_norm_biases(), "norm_b", i);
+            same(o.get_dv_weights(), r.get_dv_weights(), "dv_w", i);
+            same(o.get_dm_weights(), r.get_dm_weights(), "dm_w", i);
+            same(o.get_dv_norm_weights(), r.get_dv_norm_weights(), "dv_norm_w", i);
+            same(o.get_dm_norm_biases(), r.get_dm_norm_biases(), "dm_norm_b", i);
+            if (o.get_master_weights()) same(*o.get_master_weights(), *r.get_master_weights(), "master_w", i);
+            if (o.get_master_norm_weights())
+                same(*o.get_master_norm_weights(), *r.get_master_norm_weights(), "master_norm_w", i);
+            // loaded blocks carry the default layer config (save.rs:567-572): set it again
+            r.set_normalisation(o.get_normalisation());
+            r.set_activation(o.get_activation());
+            r.set_mask_coeff(o.get_mask_coeff());
+        }
+        FeedForwardNetwork<T> net2(std::move(back), dims[0]);
+        const std::vector<float> y1 = host_f32(ctx, *net.forward(ctx, x, batch, false, steps + 1).back());
+        const std::vector<float> y2 = host_f32(ctx, *net2.forward(ctx, x, batch, false, steps + 1).back());
+        if (std::memcmp(y1.data(), y2.data(), y1.size() * 4) != 0) throw std::runtime_error("round trip: forward");
+        std::printf("checkpoint round trip OK\n");
+    }
     std::printf("trained %zu steps\n", steps);
     return 0;
 }
@@ -284,6 +381,8 @@ int main(int argc, char **argv) {
                              std::strtoul(argv[5], nullptr, 10), std::strtoul(argv[6], nullptr, 10),
                              std::strtoul(argv[7], nullptr, 10));
         if (cmd == "ids") return ids();
+        if (cmd == "st-demo" && argc == 3) return st_demo(argv[2]);
+        if (cmd == "st-dump" && argc == 3) return st_dump(argv[2]);
         if (cmd == "train" && argc == 3) {
             const auto spec = read_spec(std::string(argv[2]) + "/spec.txt");
             return spec.at("dtype") == "f16" ? train<f16>(argv[2], spec) : train<float>(argv[2], spec);

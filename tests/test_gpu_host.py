@@ -2,8 +2,11 @@
 soklyn_tool (DenseBlock::new_with_config with InitHeNormalFunc, forward with dropout
 seeded by scramble_seed(step, weight id), compute_loss, backward_output and
 backward_hidden in the order of src/ffn.rs:113-166), checked against the oracle run on
-the same initial weights, inputs and seeds; and the tensor-id sequence of
-src/mlp.rs:46-421 (23 ids per fp32 training block, 27 per fp16 one).
+the same initial weights, inputs and seeds; the tensor-id sequence of
+src/mlp.rs:46-421 (23 ids per fp32 training block, 27 per fp16 one); and the trained
+network's checkpoint (src/io/save.rs): the tool saves it, reloads it into blocks and
+checks every tensor and the forward bit for bit, and the file itself is checked here
+with the `safetensors` library and against the reference's header layout.
 """
 from __future__ import annotations
 
@@ -17,6 +20,7 @@ from oracle import oracle as O
 from soklyn_amd import abi
 from tests.helpers import FP16_TOL, FP32_TOL, f16, normwise, rng
 from tests.test_gpu_ffn import oracle_step
+from tests.test_safetensors_cpu import serde_pretty_header
 
 pytestmark = pytest.mark.gpu
 
@@ -46,7 +50,8 @@ def run_scenario(tmp, *, dtype, dims, batch, steps, norm, act, leaky, mask_coeff
         fh.write("".join(f"{k}={v}\n" for k, v in spec.items()))
     x.astype(np.float32).tofile(os.path.join(tmp, "x.bin"))
     t.astype(np.float32).tofile(os.path.join(tmp, "t.bin"))
-    tool("train", tmp)
+    out = tool("train", tmp)
+    assert "checkpoint round trip OK" in out
     L = len(dims) - 1
     ids = [int(l) for l in open(os.path.join(tmp, "ids.txt")).read().split()]
     w0 = [np.fromfile(os.path.join(tmp, f"w{i}_init.bin"), np.float32).reshape(dims[i], dims[i + 1])
@@ -57,7 +62,40 @@ def run_scenario(tmp, *, dtype, dims, batch, steps, norm, act, leaky, mask_coeff
             path = os.path.join(tmp, f"{n}{i}.bin")
             if os.path.exists(path):
                 res[(n, i)] = np.fromfile(path, np.float32)
+    check_checkpoint(os.path.join(tmp, "net.safetensors"), dims, dtype, res, steps)
     return ids, w0, res
+
+
+def check_checkpoint(path, dims, dtype, res, steps):
+    """save.rs:227-345: names, shapes, dtypes, data order and values of the written file."""
+    from safetensors import safe_open
+    from safetensors.numpy import load_file
+    t = load_file(path)
+    tdt = "F16" if dtype == "f16" else "F32"
+    expect, off = {}, 0
+    for i in range(len(dims) - 1):
+        K, N, pre = dims[i], dims[i + 1], f"layer{i + 1}."
+        entries = [("w", tdt, (K, N)), ("b", tdt, (N,)), ("norm_w", tdt, (N,)), ("norm_b", tdt, (N,)),
+                   ("dv_w", "F32", (K, N)), ("dv_b", "F32", (N,)), ("dm_w", "F32", (K, N)), ("dm_b", "F32", (N,)),
+                   ("dv_norm_w", "F32", (N,)), ("dv_norm_b", "F32", (N,)), ("dm_norm_w", "F32", (N,)),
+                   ("dm_norm_b", "F32", (N,))]
+        if dtype == "f16":
+            entries += [("master_w", "F32", (K, N)), ("master_b", "F32", (1, N)), ("master_norm_w", "F32", (1, N)),
+                        ("master_norm_b", "F32", (1, N))]
+        for n, dt, shape in entries:
+            nbytes = int(np.prod(shape)) * (2 if dt == "F16" else 4)
+            expect[pre + n] = (dt, shape, off, off + nbytes)
+            off += nbytes
+            assert t[pre + n].shape == shape and t[pre + n].dtype == (np.float16 if dt == "F16" else np.float32), n
+        for n in ("w", "b", "dv_w", "dm_w", "dv_b") + (("master_w",) if dtype == "f16" else ()):
+            assert np.array_equal(t[pre + n].astype(np.float32).reshape(-1), res[(n, i)]), f"layer {i} {n}"
+    assert set(t) == set(expect)
+    blob = open(path, "rb").read()
+    n = int(np.frombuffer(blob[:8], "<u8")[0])
+    assert blob[8:8 + n] == serde_pretty_header(expect, {"steps": str(steps)})
+    assert len(blob) == 8 + n + off
+    with safe_open(path, "np") as f:
+        assert f.metadata() == {"steps": str(steps)}
 
 
 def oracle_net(dims, batch, half, w0, hidden_kw):

@@ -15,6 +15,19 @@
 
 using namespace skl;
 
+// Column sums of d_prenorm / dNorm_w / dNorm_b (partials [splits x 3 x n])
+// written by an error entry point as a by-product of its pass over the rows.
+// skl_dense_backward uses them instead of reading the three buffers again when
+// they describe the same block and batch and were made by the call just
+// before it on this context (every entry point counts as a call, so anything
+// issued through the context in between invalidates them).
+struct ColSums {
+    const float *dp, *dnw, *dnb;
+    uint32_t rows, n, splits, norm;
+    uint64_t call;
+    bool valid;
+};
+
 struct skl_ctx {
     int device;
     uint32_t tile_dim;
@@ -23,6 +36,10 @@ struct skl_ctx {
     uint32_t sync;
     void *ws;
     size_t ws_bytes;
+    uint64_t calls;      // entry-point calls so far
+    float *cols;         // ColSums storage
+    size_t cols_bytes;
+    ColSums cs;
 };
 
 namespace {
@@ -48,20 +65,52 @@ int32_t finish(skl_ctx *ctx) {
 
 int32_t enter(skl_ctx *ctx) {
     if (!ctx) return SKL_ERR_NULL_POINTER;
+    ++ctx->calls;
     SKL_TRY(hipSetDevice(ctx->device));
     return SKL_OK;
 }
 
-int32_t ensure_ws(skl_ctx *ctx, size_t bytes) {
-    if (bytes <= ctx->ws_bytes) return SKL_OK;
+// Grow a context-owned device buffer (work in flight may still use it: sync first).
+int32_t ensure_buf(skl_ctx *ctx, void **buf, size_t *have, size_t bytes) {
+    if (bytes <= *have) return SKL_OK;
     SKL_TRY(hipStreamSynchronize(ctx->stream));
-    if (ctx->ws) SKL_TRY(hipFree(ctx->ws));
-    ctx->ws = nullptr;
-    ctx->ws_bytes = 0;
-    size_t want = bytes + (bytes >> 3);
-    SKL_TRY(hipMalloc(&ctx->ws, want));
-    ctx->ws_bytes = want;
+    if (*buf) SKL_TRY(hipFree(*buf));
+    *buf = nullptr;
+    *have = 0;
+    const size_t want = bytes + (bytes >> 3);
+    SKL_TRY(hipMalloc(buf, want));
+    *have = want;
     return SKL_OK;
+}
+
+int32_t ensure_ws(skl_ctx *ctx, size_t bytes) { return ensure_buf(ctx, &ctx->ws, &ctx->ws_bytes, bytes); }
+
+// Room for the column sums of an error call over [rows x n]; returns the splits.
+int32_t ensure_cols(skl_ctx *ctx, uint32_t rows, uint32_t n, uint32_t *splits) {
+    *splits = err_col_splits(rows, n);
+    void *p = ctx->cols;
+    const int32_t r = ensure_buf(ctx, &p, &ctx->cols_bytes, (size_t)*splits * 3 * n * sizeof(float));
+    ctx->cols = reinterpret_cast<float *>(p);
+    return r;
+}
+
+void record_cols(skl_ctx *ctx, const skl_dense_desc *b, uint32_t rows, uint32_t splits) {
+    ColSums &c = ctx->cs;
+    c.dp = b->d_prenorm;
+    c.dnw = b->d_norm_w;
+    c.dnb = b->d_norm_b;
+    c.rows = rows;
+    c.n = b->outputs;
+    c.splits = splits;
+    c.norm = b->norm;
+    c.call = ctx->calls;
+    c.valid = true;
+}
+
+bool cols_match(const skl_ctx *ctx, const skl_dense_desc *b, uint32_t rows) {
+    const ColSums &c = ctx->cs;
+    return c.valid && c.call + 1 >= ctx->calls && c.dp == b->d_prenorm && c.rows == rows && c.n == b->outputs &&
+           c.norm == b->norm && (b->norm == SKL_NORM_DISABLED || (c.dnw == b->d_norm_w && c.dnb == b->d_norm_b));
 }
 
 size_t elem_size(uint32_t dtype) { return dtype == SKL_F16 ? 2 : 4; }
@@ -204,6 +253,7 @@ int32_t skl_ctx_destroy(skl_ctx *ctx) {
     hipSetDevice(ctx->device);
     hipStreamSynchronize(ctx->stream);
     if (ctx->ws) hipFree(ctx->ws);
+    if (ctx->cols) hipFree(ctx->cols);
     hipStreamDestroy(ctx->own_stream);
     delete ctx;
     return SKL_OK;
@@ -413,7 +463,11 @@ int32_t skl_dense_output_error(skl_ctx *ctx, const skl_dense_desc *b, const void
     a.d_norm_w = b->d_norm_w;
     a.d_norm_b = b->d_norm_b;
     a.d_prenorm_h = b->dtype == SKL_F16 ? reinterpret_cast<half_t *>(b->d_prenorm_h) : nullptr;
-    SKL_TRY(launch_output_error(a, ctx->stream));
+    uint32_t splits = 0;
+    if ((r = ensure_cols(ctx, target_rows, b->outputs, &splits))) return r;
+    bool sums = false;
+    SKL_TRY(launch_output_error(a, ctx->cols, splits, &sums, ctx->stream));
+    if (sums) record_cols(ctx, b, target_rows, splits);
     return finish(ctx);
 }
 
@@ -436,6 +490,7 @@ static int32_t hidden_error_impl(skl_ctx *ctx, const skl_dense_desc *cur, const 
         if (cur->norm) SKL_CHECK(cur->master_norm_w, SKL_ERR_NULL_POINTER);
     }
     if ((r = zero_dnorm_tail(ctx, cur, batch))) return r;
+    ctx->cs.valid = false;   // cur's d_prenorm is rewritten without column sums
 
     GemmLaunch g{};
     g.dtype = cur->dtype;
@@ -540,8 +595,10 @@ static int32_t backward_impl(skl_ctx *ctx, const skl_dense_desc *b, const void *
         if (splits < 2) splits = 1;
     }
 
-    // column partial sums for db / dNorm sums share the workspace
-    const uint32_t csplits = colsum_splits(batch, N);
+    // column partial sums for db / dNorm sums: left by the error call just
+    // before, or made here in the workspace
+    const bool cached = cols_match(ctx, b, batch);
+    const uint32_t csplits = cached ? ctx->cs.splits : colsum_splits(batch, N);
 
     GemmLaunch g{};
     g.dtype = b->dtype;
@@ -562,7 +619,7 @@ static int32_t backward_impl(skl_ctx *ctx, const skl_dense_desc *b, const void *
                             use_transposed_operands(b->dtype, K, N, batch, in_cols) && aligned16(in) &&
                             aligned16(b->d_prenorm_h);
     const size_t dw_bytes = splits > 1 ? (size_t)splits * K * N * sizeof(float) : 0;
-    const size_t col_bytes = (size_t)csplits * 3 * N * sizeof(float);
+    const size_t col_bytes = cached ? 0 : (size_t)csplits * 3 * N * sizeof(float);
     const size_t xt_bytes = transposed ? (size_t)K * batch * sizeof(uint16_t) : 0;
     const size_t pt_bytes = transposed ? (size_t)N * batch * sizeof(uint16_t) : 0;
     if ((r = ensure_ws(ctx, dw_bytes + col_bytes + xt_bytes + pt_bytes))) return r;
@@ -612,7 +669,7 @@ static int32_t backward_impl(skl_ctx *ctx, const skl_dense_desc *b, const void *
     v.src[0] = use_bias ? b->d_prenorm : nullptr;
     v.src[1] = b->norm > 0 ? b->d_norm_w : nullptr;
     v.src[2] = b->norm > 1 ? b->d_norm_b : nullptr;
-    v.partials = ws_col;
+    v.partials = cached ? ctx->cols : ws_col;
     void *params[3] = {b->b, b->norm_w, b->norm_b};
     float *masters[3] = {b->master_b, b->master_norm_w, b->master_norm_b};
     float *dvs[3] = {b->dv_b, b->dv_norm_w, b->dv_norm_b};
@@ -629,7 +686,7 @@ static int32_t backward_impl(skl_ctx *ctx, const skl_dense_desc *b, const void *
     v.clamp = t->grad_clamp;
     v.inv_m = inv_m;
     if (v.enabled[0] || v.enabled[1] || v.enabled[2]) {
-        SKL_TRY(launch_colsum(v, ctx->stream));
+        if (!cached) SKL_TRY(launch_colsum(v, ctx->stream));
         SKL_TRY(launch_vec_opt(v, ctx->stream));
     }
     return SKL_OK;
@@ -692,7 +749,11 @@ int32_t skl_dense_error_from_sum(skl_ctx *ctx, const skl_dense_desc *b, const fl
     a.d_norm_w = b->d_norm_w;
     a.d_norm_b = b->d_norm_b;
     a.d_prenorm_h = b->dtype == SKL_F16 ? reinterpret_cast<half_t *>(b->d_prenorm_h) : nullptr;
-    SKL_TRY(launch_error_from_sum(a, ctx->stream));
+    uint32_t splits = 0;
+    if ((r = ensure_cols(ctx, batch, b->outputs, &splits))) return r;
+    bool sums = false;
+    SKL_TRY(launch_error_from_sum(a, ctx->cols, splits, &sums, ctx->stream));
+    if (sums) record_cols(ctx, b, batch, splits);
     return finish(ctx);
 }
 

@@ -276,81 +276,125 @@ template <typename T> __global__ void error_from_sum_kernel(ErrArgs a) {
 
 // Vector forms: each thread owns 4 consecutive elements of one row (n % 4 == 0,
 // 16-byte aligned buffers): 16-byte fp32 / 8-byte fp16 accesses, 32-bit indexing.
+// The three values of one 4-column group that feed the column sums of backward.cu:187-194.
+struct ErrSums4 {
+    f32x4 dp, dnw, dnb;
+};
+
 template <typename T>
-__device__ __forceinline__ void write_err4(const ErrArgs &a, uint64_t idx, uint32_t row, uint32_t col, f32x4 e) {
+__device__ __forceinline__ ErrSums4 write_err4(const ErrArgs &a, uint64_t idx, uint32_t row, uint32_t col, f32x4 e) {
     __builtin_nontemporal_store(e, reinterpret_cast<f32x4 *>(a.grad + idx));
-    f32x4 dp = e;
+    ErrSums4 o;
+    o.dp = e;
+    o.dnw = o.dnb = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     if (a.norm) {
         const f32x4 pv = a.norm == 1 ? load4<T>(a.prenorm, idx) : f32x4{0, 0, 0, 0};
         const f32x4 cv = a.norm >= 2 ? load4<T>(a.centered, idx) : f32x4{0, 0, 0, 0};
         const f32x4 nw = *reinterpret_cast<const f32x4 *>(a.nw + col);
-        f32x4 dnw, dnb;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const float rstd = to_f32(ldv<T>(a.norm_rstd, a.norm == 3 ? col + j : row));
             const NormGrad g = norm_grad(a.norm, e[j], pv[j], cv[j], rstd, nw[j], a.inv_n, a.inv_m);
-            dp[j] = g.d_prenorm;
-            dnw[j] = g.dnw;
-            dnb[j] = g.dnb;
+            o.dp[j] = g.d_prenorm;
+            o.dnw[j] = g.dnw;
+            o.dnb[j] = g.dnb;
         }
-        *reinterpret_cast<f32x4 *>(a.d_norm_w + idx) = dnw;
-        *reinterpret_cast<f32x4 *>(a.d_norm_b + idx) = dnb;
+        *reinterpret_cast<f32x4 *>(a.d_norm_w + idx) = o.dnw;
+        *reinterpret_cast<f32x4 *>(a.d_norm_b + idx) = o.dnb;
     }
-    dp = dp * a.loss_scale;
-    __builtin_nontemporal_store(dp, reinterpret_cast<f32x4 *>(a.d_prenorm + idx));
-    if (a.d_prenorm_h) store4<half_t>(a.d_prenorm_h, idx, dp);
+    o.dp = o.dp * a.loss_scale;
+    __builtin_nontemporal_store(o.dp, reinterpret_cast<f32x4 *>(a.d_prenorm + idx));
+    if (a.d_prenorm_h) store4<half_t>(a.d_prenorm_h, idx, o.dp);
+    return o;
 }
 
-template <typename T> __global__ void __launch_bounds__(256) output_error_vec_kernel(ErrArgs a) {
-    const uint32_t nv = a.n >> 2, total = a.rows * nv;
-    for (uint32_t q = blockIdx.x * blockDim.x + threadIdx.x; q < total; q += gridDim.x * blockDim.x) {
-        const uint32_t row = q / nv, col = (q - row * nv) << 2;
-        const uint64_t idx = (uint64_t)row * a.n + col;
-        const f32x4 out = load4<T>(a.out, idx), tg = load4<T>(a.target, idx), pre = load4<T>(a.preact, idx);
-        f32x4 e;
+// Loss delta of one 4-column group (backward.cu:24-45).
+template <typename T> __device__ __forceinline__ f32x4 output_err4(const ErrArgs &a, uint64_t idx) {
+    const f32x4 out = load4<T>(a.out, idx), tg = load4<T>(a.target, idx), pre = load4<T>(a.preact, idx);
+    f32x4 e;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float o = activation(a.act, out[j], a.leaky);
-            float ej = 0.0f;
-            if (a.loss == 0) {
-                ej = activation_derivative(a.act, o - tg[j], o, pre[j], a.leaky);
-            } else if ((a.loss == 1 && a.act == 5) || (a.loss == 2 && a.act == 1)) {
-                ej = o - tg[j];
+    for (int j = 0; j < 4; ++j) {
+        const float o = activation(a.act, out[j], a.leaky);
+        float ej = 0.0f;
+        if (a.loss == 0) {
+            ej = activation_derivative(a.act, o - tg[j], o, pre[j], a.leaky);
+        } else if ((a.loss == 1 && a.act == 5) || (a.loss == 2 && a.act == 1)) {
+            ej = o - tg[j];
+        }
+        e[j] = ej;
+    }
+    return e;
+}
+
+// Error + column sums in one pass.  Workgroup (x, y) owns the columns
+// [1024 UC x, 1024 UC (x + 1)) of the rows [y per, (y + 1) per): a thread owns
+// UC 4-column groups 1024 apart, loads UR rows of all of them before computing
+// any (UR x UC x 40 bytes in flight), writes grad / d_prenorm (/ dNorm) and
+// adds d_prenorm, dNorm_w and dNorm_b into running column sums, rows in
+// ascending order.  The sums go to partials[y][k][n] (k = 0 d_prenorm,
+// 1 dNorm_w, 2 dNorm_b; 1 and 2 only with a norm), the inputs of the bias /
+// norm-parameter update, so the backward does not read the three [rows x n]
+// buffers again.
+template <typename T, bool FROM_SUM, int UR, int UC>
+__global__ void __launch_bounds__(256) error_cols_kernel(ErrArgs a, float *__restrict__ partials, uint32_t per) {
+    const uint32_t cbase = blockIdx.x * (1024 * UC) + threadIdx.x * 4;
+    if (cbase >= a.n) return;
+    const uint32_t r0 = blockIdx.y * per;
+    const uint32_t r1 = min(a.rows, r0 + per);
+    f32x4 sdp[UC], snw[UC], snb[UC];
+#pragma unroll
+    for (int v = 0; v < UC; ++v) sdp[v] = snw[v] = snb[v] = f32x4{0, 0, 0, 0};
+    for (uint32_t rb = r0; rb < r1; rb += UR) {
+        f32x4 x0[UR][UC], x1[UR][UC], x2[UR][UC], x3[UR][UC];
+        if constexpr (FROM_SUM) {
+#pragma unroll
+            for (int u = 0; u < UR; ++u) {
+                if (rb + u >= r1) break;
+#pragma unroll
+                for (int v = 0; v < UC; ++v) {
+                    const uint32_t c = cbase + 1024 * v;
+                    if (c >= a.n) break;
+                    const uint32_t idx = (rb + u) * a.n + c;
+                    x0[u][v] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(a.s + idx));
+                    x1[u][v] = load4<T>(a.predrop, idx);
+                    x2[u][v] = load4<T>(a.preact, idx);
+                    x3[u][v] = load4<T>(a.mask, idx);
+                }
             }
-            e[j] = ej;
         }
-        write_err4<T>(a, idx, row, col, e);
+#pragma unroll
+        for (int u = 0; u < UR; ++u) {
+            const uint32_t row = rb + u;
+            if (row >= r1) break;
+#pragma unroll
+            for (int v = 0; v < UC; ++v) {
+                const uint32_t c = cbase + 1024 * v;
+                if (c >= a.n) break;
+                const uint32_t idx = row * a.n + c;
+                f32x4 e;
+                if constexpr (FROM_SUM) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        e[j] = x3[u][v][j] * activation_derivative(a.act, x0[u][v][j], x1[u][v][j], x2[u][v][j], a.leaky);
+                } else {
+                    e = output_err4<T>(a, idx);
+                }
+                const ErrSums4 o = write_err4<T>(a, idx, row, c, e);
+                sdp[v] += o.dp;
+                snw[v] += o.dnw;
+                snb[v] += o.dnb;
+            }
+        }
     }
-}
-
-// A workgroup owns ERR_U x 256 consecutive 4-element groups; a thread loads all
-// ERR_U of its groups before computing any, so each keeps ERR_U x 40 bytes in flight.
-constexpr int ERR_U = 4;
-template <typename T> __global__ void __launch_bounds__(256) error_from_sum_vec_kernel(ErrArgs a) {
-    const uint32_t nv = a.n >> 2, total = a.rows * nv;
-    for (uint32_t q0 = blockIdx.x * (ERR_U * 256) + threadIdx.x; q0 < total; q0 += gridDim.x * (ERR_U * 256)) {
-        f32x4 s[ERR_U], pd[ERR_U], pa[ERR_U], mk[ERR_U];
 #pragma unroll
-        for (int u = 0; u < ERR_U; ++u) {
-            const uint32_t q = q0 + u * 256;
-            if (q >= total) break;
-            const uint32_t row = q / nv, col = (q - row * nv) << 2;
-            const uint64_t idx = (uint64_t)row * a.n + col;
-            s[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(a.s + idx));
-            pd[u] = load4<T>(a.predrop, idx);
-            pa[u] = load4<T>(a.preact, idx);
-            mk[u] = load4<T>(a.mask, idx);
-        }
-#pragma unroll
-        for (int u = 0; u < ERR_U; ++u) {
-            const uint32_t q = q0 + u * 256;
-            if (q >= total) break;
-            const uint32_t row = q / nv, col = (q - row * nv) << 2;
-            f32x4 e;
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                e[j] = mk[u][j] * activation_derivative(a.act, s[u][j], pd[u][j], pa[u][j], a.leaky);
-            write_err4<T>(a, (uint64_t)row * a.n + col, row, col, e);
+    for (int v = 0; v < UC; ++v) {
+        const uint32_t c = cbase + 1024 * v;
+        if (c >= a.n) break;
+        float *p = partials + (uint64_t)blockIdx.y * 3 * a.n + c;
+        *reinterpret_cast<f32x4 *>(p) = sdp[v];
+        if (a.norm) {
+            *reinterpret_cast<f32x4 *>(p + a.n) = snw[v];
+            *reinterpret_cast<f32x4 *>(p + 2 * a.n) = snb[v];
         }
     }
 }
@@ -368,37 +412,56 @@ static bool err_vec_ok(const ErrArgs &a, bool from_sum) {
     return true;
 }
 
-hipError_t launch_output_error(const ErrArgs &a, hipStream_t s) {
+// 4 rows x 1 column group per thread and ~1024 workgroups: of the shapes
+// measured on the C3 step (UR x UC in {4x1, 2x2, 1x4, 2x4}, 512 to 2048
+// workgroups) the fastest, both alone and between the GEMMs of the step.
+constexpr int ERR_UR = 4, ERR_UC = 1;
+
+// Row splits of the fused error + column-sum kernels: ~1024 workgroups.
+uint32_t err_col_splits(uint32_t rows, uint32_t n) {
+    const uint32_t col_blocks = cdiv(n, 1024 * ERR_UC);
+    uint32_t sp = cdiv(1024, col_blocks);
+    const uint32_t cap = cdiv(rows, 16);
+    if (sp > cap) sp = cap;
+    if (sp > 1024) sp = 1024;
+    return sp < 1 ? 1 : sp;
+}
+
+template <bool FROM_SUM>
+static hipError_t launch_error(const ErrArgs &a, float *partials, uint32_t splits, hipStream_t s) {
     const uint64_t total = (uint64_t)a.rows * a.n;
     if (total == 0) return hipSuccess;
-    if (err_vec_ok(a, false)) {
+    if (partials) {
+        const uint32_t per = cdiv(a.rows, splits);
+        const dim3 g(cdiv(a.n, 1024 * ERR_UC), splits);
         if (a.dtype == 1)
-            hipLaunchKernelGGL(output_error_vec_kernel<half_t>, grid_for(total / 4, 256), dim3(256), 0, s, a);
+            hipLaunchKernelGGL((error_cols_kernel<half_t, FROM_SUM, ERR_UR, ERR_UC>), g, dim3(256), 0, s, a,
+                               partials, per);
         else
-            hipLaunchKernelGGL(output_error_vec_kernel<float>, grid_for(total / 4, 256), dim3(256), 0, s, a);
-    } else if (a.dtype == 1) {
-        hipLaunchKernelGGL(output_error_kernel<half_t>, grid_for(total, 256), dim3(256), 0, s, a);
+            hipLaunchKernelGGL((error_cols_kernel<float, FROM_SUM, ERR_UR, ERR_UC>), g, dim3(256), 0, s, a,
+                               partials, per);
+    } else if (FROM_SUM) {
+        if (a.dtype == 1)
+            hipLaunchKernelGGL(error_from_sum_kernel<half_t>, grid_for(total, 256), dim3(256), 0, s, a);
+        else
+            hipLaunchKernelGGL(error_from_sum_kernel<float>, grid_for(total, 256), dim3(256), 0, s, a);
     } else {
-        hipLaunchKernelGGL(output_error_kernel<float>, grid_for(total, 256), dim3(256), 0, s, a);
+        if (a.dtype == 1)
+            hipLaunchKernelGGL(output_error_kernel<half_t>, grid_for(total, 256), dim3(256), 0, s, a);
+        else
+            hipLaunchKernelGGL(output_error_kernel<float>, grid_for(total, 256), dim3(256), 0, s, a);
     }
     return hipGetLastError();
 }
 
-hipError_t launch_error_from_sum(const ErrArgs &a, hipStream_t s) {
-    const uint64_t total = (uint64_t)a.rows * a.n;
-    if (total == 0) return hipSuccess;
-    if (err_vec_ok(a, true)) {
-        const dim3 g = grid_for(total / 4, 256 * ERR_U);
-        if (a.dtype == 1)
-            hipLaunchKernelGGL(error_from_sum_vec_kernel<half_t>, g, dim3(256), 0, s, a);
-        else
-            hipLaunchKernelGGL(error_from_sum_vec_kernel<float>, g, dim3(256), 0, s, a);
-    } else if (a.dtype == 1) {
-        hipLaunchKernelGGL(error_from_sum_kernel<half_t>, grid_for(total, 256), dim3(256), 0, s, a);
-    } else {
-        hipLaunchKernelGGL(error_from_sum_kernel<float>, grid_for(total, 256), dim3(256), 0, s, a);
-    }
-    return hipGetLastError();
+hipError_t launch_output_error(const ErrArgs &a, float *partials, uint32_t splits, bool *sums, hipStream_t s) {
+    *sums = partials && err_vec_ok(a, false);
+    return launch_error<false>(a, *sums ? partials : nullptr, splits, s);
+}
+
+hipError_t launch_error_from_sum(const ErrArgs &a, float *partials, uint32_t splits, bool *sums, hipStream_t s) {
+    *sums = partials && err_vec_ok(a, true);
+    return launch_error<true>(a, *sums ? partials : nullptr, splits, s);
 }
 
 // ---- column sums (backward.cu:187-194) + vector optimiser (backward.cu:198-225) -------
@@ -418,7 +481,8 @@ __global__ void __launch_bounds__(256) colsum_kernel(VecOptArgs a) {
 }
 
 // 16 columns per workgroup, 16 lanes per column: lane j sums the partials of
-// splits j, j+16, ... in order, then the 16 are added in a fixed pairwise order.
+// splits j, j+16, ... in order (four loads in flight per batch), then the 16
+// are added in a fixed pairwise order.
 template <typename T> __global__ void __launch_bounds__(256) vec_opt_kernel(VecOptArgs a) {
     __shared__ float red[3][16][17];
     const uint32_t cl = threadIdx.x & 15u, j = threadIdx.x >> 4;
@@ -426,8 +490,19 @@ template <typename T> __global__ void __launch_bounds__(256) vec_opt_kernel(VecO
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
         float s = 0.0f;
-        if (a.enabled[k] && col < a.n)
-            for (uint32_t sp = j; sp < a.splits; sp += 16) s += a.partials[((uint64_t)sp * 3 + k) * a.n + col];
+        if (a.enabled[k] && col < a.n) {
+            const float *p = a.partials + (uint64_t)k * a.n + col;
+            const uint64_t st = (uint64_t)3 * a.n;   // between splits
+            uint32_t sp = j;
+            for (; sp + 48 < a.splits; sp += 64) {
+                const float v0 = p[sp * st], v1 = p[(sp + 16) * st], v2 = p[(sp + 32) * st], v3 = p[(sp + 48) * st];
+                s += v0;
+                s += v1;
+                s += v2;
+                s += v3;
+            }
+            for (; sp < a.splits; sp += 16) s += p[sp * st];
+        }
         red[k][j][cl] = s;
     }
     __syncthreads();

@@ -411,8 +411,12 @@ static bool dma_ok(const GemmLaunch &g) {
 
 bool gemm_direct_ok(const GemmLaunch &g) { return gemm_large_tile(g.dtype, g.M, g.N) && dma_ok(g); }
 
+// Waves per workgroup: 8 when an operand is read through the transposing LDS
+// path (its 8-byte reads leave one wave per SIMD waiting on LDS latency), 4
+// when both operands are k-contiguous (see gemm_dma.h).
 template <class Epi, bool AK, bool BK_>
 static hipError_t run_dma(const GemmLaunch &g, const typename Epi::Params &p, hipStream_t s) {
+    constexpr int NW = (AK && BK_) ? 4 : 8;
     GemmShape sh{};
     sh.M = g.M;
     sh.N = g.N;
@@ -425,7 +429,7 @@ static hipError_t run_dma(const GemmLaunch &g, const typename Epi::Params &p, hi
     const dim3 grid(sh.tiles_m * sh.tiles_n);
     const half_t *A = reinterpret_cast<const half_t *>(g.A);
     const half_t *B = reinterpret_cast<const half_t *>(g.B);
-    hipLaunchKernelGGL((gemm_dma_kernel<Epi, AK, BK_>), grid, dim3(Dma256::NT), 0, s, sh, A, B, p);
+    hipLaunchKernelGGL((gemm_dma_kernel<Epi, AK, BK_, NW>), grid, dim3(DmaCfg<NW>::NT), 0, s, sh, A, B, p);
     return hipGetLastError();
 }
 

@@ -3,15 +3,20 @@
 // m/n-contiguous (the forward's W, both operands of dW), so no layout needs a
 // transposed copy.
 //
-//  * 4 waves (1 per SIMD), wave tile 128 x 128 = 4 x 4 v_mfma_f32_32x32x16_f16
-//    blocks; the 256 accumulators live in AGPRs, fragments in VGPRs.  Per
-//    k-step a wave reads 8 x 1 KB fragments from LDS for 16 MFMAs, a third
-//    less LDS read traffic per flop than a 128 x 64 wave tile.
+//  * NW = 4 or 8 waves.  NW = 4: one wave per SIMD, wave tile 128 x 128 =
+//    4 x 4 v_mfma_f32_32x32x16_f16 blocks, 256 accumulators per lane in AGPRs;
+//    per k-step a wave reads 8 x 1 KB fragments for 16 MFMAs.  NW = 8: two
+//    waves per SIMD, wave tile 128 x 64 (4 x 2 blocks, 128 accumulators), 1.5x
+//    the LDS fragment bytes per flop, but while one wave of a SIMD waits on its
+//    LDS reads the other issues MFMAs.  Measured on the C3 shapes (random fp16
+//    data, 20 launches back to back): 8 waves run the layouts with a
+//    transposing (m/n-contiguous) operand 6-7% faster, and the all-k-contiguous
+//    layout 1-3% slower, so the launcher picks per layout.
 //  * BK = 64 halves; 2 stages of 64 KB (A tile + B tile, 32 KB each, laid out
 //    per operand layout as described at OpK / OpN).  Stages are filled by
 //    global_load_lds_dwordx4 (no staging registers, no ds_write): one wave
 //    instruction fills 1 KB of LDS, each lane fetching the global chunk that
-//    the swizzle puts in its slot.
+//    the swizzle puts in its slot; a wave issues 32 / NW per operand per tile.
 //  * Fragments are software-pipelined across the per-tile barrier: the four
 //    k-steps of a tile alternate between two fragment register sets, and the
 //    MFMAs of a tile's last k-step are issued after the barrier, behind the
@@ -24,14 +29,14 @@
 //    allocator spill): K is a multiple of 2 k-tiles, the last two
 //    refills fetch the final k-tile again (in bounds, never read), and the last
 //    cross-barrier fragment read lands in registers nobody reads.
-//  * Fragment reads are inline ds_read_b128 (left to itself the compiler sinks
-//    each read next to its first MFMA behind an lgkmcnt(0), serialising LDS
-//    latency with the MFMA pipe).  The compiler does not count them, so the
-//    kernel waits for them itself: before a fragment set is consumed at most
-//    the other set's 8 reads may be pending (LDS returns in order; a scalar
-//    load in flight only makes the wait stricter), and the wait is an asm
-//    statement that rewrites the set's registers, so no MFMA can be scheduled
-//    above it.
+//  * Fragment reads are inline ds_read_b128 / ds_read_b64_tr_b16 (left to
+//    itself the compiler sinks each read next to its first MFMA behind an
+//    lgkmcnt(0), serialising LDS latency with the MFMA pipe).  The compiler
+//    does not count them, so the kernel waits for them itself: before a
+//    fragment set is consumed at most the other set's reads may be pending
+//    (LDS returns in order; a scalar load in flight only makes the wait
+//    stricter), and after the wait an empty asm statement per fragment
+//    register claims to rewrite it, so no MFMA can be scheduled above the wait.
 // Operand offsets are 32-bit (rows * ld * 2 bytes < 4 GiB).
 #pragma once
 
@@ -39,12 +44,13 @@
 
 namespace skl {
 
-struct Dma256 {
-    static constexpr int BM = 256, BN = 256, BK = 64, WM = 2, WN = 2, NT = 256, NWAVES = 4;
+template <int NW_> struct DmaCfg {
+    static_assert(NW_ == 4 || NW_ == 8, "4 or 8 waves");
+    static constexpr int NW = NW_;
+    static constexpr int BM = 256, BN = 256, BK = 64, WM = 2, WN = NW / 2, NT = 64 * NW;
     static constexpr int TWM = BM / WM, TWN = BN / WN, MT = TWM / 32, NTL = TWN / 32;
     static constexpr int OPB = 256 * BK * 2;       // 32 KB per operand tile
     static constexpr int STAGEB = 2 * OPB;         // 64 KB per stage
-    static constexpr int IPO = OPB / 1024 / NWAVES;   // 8 DMA instructions per operand per wave
 };
 
 typedef __attribute__((address_space(3))) char lds_char;
@@ -72,34 +78,39 @@ template <int OFF> __device__ __forceinline__ void ds_read16(u32x4 &dst, uint32_
 template <int OFF> __device__ __forceinline__ void ds_read8_tr(u32x2 &dst, uint32_t addr) {
     asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(dst) : "v"(addr), "i"(OFF) : "memory");
 }
+// Claims to rewrite v: orders every later use of v after the preceding asm.
+__device__ __forceinline__ void pin(u32x4 &v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void pin(u32x2 &v) { asm volatile("" : "+v"(v)); }
 
 // ---- operand staging ------------------------------------------------------------
-// One operand tile of a stage: 256 rows (m or n) x 64 k, 32 KB, filled by 8
-// global_load_lds_dwordx4 per wave (one wave instruction = 1 KB of LDS, lane l
-// writing bytes 16 l .. 16 l + 15), read as four 32-row MFMA fragments of the
-// wave's 128 rows per k-step.  The fragment of a lane holds 8 consecutive k of
-// row l % 32 (k = 8 (l / 32) .. + 7 within the 16-k step).
+// One operand tile of a stage: 256 rows (m or n) x 64 k, 32 KB, filled by
+// global_load_lds_dwordx4 (one wave instruction = 1 KB of LDS, lane l writing
+// bytes 16 l .. 16 l + 15; instruction t of wave w fills KB NW t + w), read
+// as NF 32-row MFMA fragments of the wave's rows per k-step.  The fragment of
+// a lane holds 8 consecutive k of row l % 32 (k = 8 (l / 32) .. + 7 within
+// the 16-k step).
 //
 // OpK: k-contiguous in HBM (row r at p + r ld).  LDS row = 128 bytes = 8
 // chunks of 8 halves, chunk c of row r stored at slot c ^ ((r >> 1) & 7): any
 // 16 consecutive rows of one chunk column hit 16 distinct 16-byte bank groups.
 // A fragment is one ds_read_b128.
-struct OpK {
-    static constexpr int READS = 4;   // ds_read per k-step
-    struct Frag { u32x4 v[4]; };
+template <int NW, int NF> struct OpK {
+    static constexpr int READS = NF;   // ds_read per k-step
+    static constexpr int IPO = 32 / NW;   // DMA instructions per tile and wave
+    struct Frag { u32x4 v[NF]; };
     const char *src;                  // DMA source of this lane, t = 0, k-tile 0
-    uint32_t step;                    // bytes between DMA instructions (32 rows)
+    uint32_t step;                    // bytes between DMA instructions (8 NW rows)
     uint32_t lds;                     // LDS byte address of this lane's fragment row, stage 0
     uint32_t g;                       // swizzle term of the fragment row
 
     __device__ __forceinline__ void init(const half_t *p, uint32_t ld, uint32_t mn0, uint32_t wbase,
                                          uint32_t wave, uint32_t lane, uint32_t lds_op) {
-        // instruction t fills rows 32 t + 8 wave .. + 7; lane -> row + lane / 8, slot lane % 8;
-        // (row >> 1) & 7 does not depend on t
+        // instruction t fills rows 8 (NW t + wave) .. + 7; lane -> row + lane / 8, slot lane % 8;
+        // (row >> 1) & 7 does not depend on t (8 NW t >> 1 is a multiple of 8)
         const uint32_t row0 = 8u * wave + (lane >> 3);
         const uint32_t kc = (lane & 7u) ^ ((row0 >> 1) & 7u);
         src = reinterpret_cast<const char *>(p) + ((size_t)(mn0 + row0) * ld * 2u + kc * 16u);
-        step = 32u * ld * 2u;
+        step = 8u * NW * ld * 2u;
         const uint32_t frow = lane & 31u;
         g = (lane >> 5) ^ ((frow >> 1) & 7u);
         lds = lds_op + (wbase + frow) * 128u;
@@ -107,17 +118,23 @@ struct OpK {
     __device__ __forceinline__ void issue(int kt, lds_char *dst) const {
         const char *s = src + (uint32_t)kt * 128u;
 #pragma unroll
-        for (int t = 0; t < Dma256::IPO; ++t) dma16(s + t * step, dst + t * 4096u);
+        for (int t = 0; t < IPO; ++t) dma16(s + t * step, dst + t * (NW * 1024u));
     }
-    // logical chunk 2 ks + (lane / 32) of each fragment row
+    // logical chunk 2 ks + (lane / 32) of each fragment row; fragment i is 32 rows further on
     __device__ __forceinline__ void read(Frag &f, uint32_t stage_off, int ks) const {
         const uint32_t a = lds + stage_off + ((2u * ks) ^ g) * 16u;
         ds_read16<0 * 4096>(f.v[0], a);
         ds_read16<1 * 4096>(f.v[1], a);
-        ds_read16<2 * 4096>(f.v[2], a);
-        ds_read16<3 * 4096>(f.v[3], a);
+        if constexpr (NF > 2) {
+            ds_read16<2 * 4096>(f.v[2], a);
+            ds_read16<3 * 4096>(f.v[3], a);
+        }
     }
     __device__ __forceinline__ static u32x4 op(const Frag &f, int i) { return f.v[i]; }
+    __device__ __forceinline__ static void pin_all(Frag &f) {
+#pragma unroll
+        for (int i = 0; i < NF; ++i) pin(f.v[i]);
+    }
 };
 
 // OpN: m- (or n-) contiguous in HBM (k-row k at p + k ld).  LDS holds the
@@ -128,84 +145,68 @@ struct OpK {
 // 4 consecutive k of its own row; h = 0, 1 give k 0..3 and 4..7.  The 32 lanes
 // of a half-wave read 4 k-rows x 64 bytes, which the swizzle spreads over the
 // 4 distinct 64-byte bank windows.  Fragment i of the wave sits 32 rows
-// further on: chunk + 4 i, i.e. the lane's address XOR 64 i.
-struct OpN {
-    static constexpr int READS = 8;
-    struct Frag { u32x2 v[4][2]; };
+// further on: chunk + 4 i, i.e. the lane's address XOR 64 i (the wave's first
+// row is a multiple of 32 NF, so the chunk bits that i flips start clear).
+template <int NW, int NF> struct OpN {
+    static constexpr int READS = 2 * NF;
+    static constexpr int IPO = 32 / NW;
+    struct Frag { u32x2 v[NF][2]; };
     const char *src;
-    uint32_t step;                    // 8 k-rows per DMA instruction of a wave
+    uint32_t step;                    // 2 NW k-rows per DMA instruction of a wave
     uint32_t kstep;                   // bytes per k-tile (64 k-rows)
-    uint32_t lds[4];                  // per fragment i, stage 0, k-step 0, h = 0
+    uint32_t lds[NF];                 // per fragment i, stage 0, k-step 0, h = 0
 
     __device__ __forceinline__ void init(const half_t *p, uint32_t ld, uint32_t mn0, uint32_t wbase,
                                          uint32_t wave, uint32_t lane, uint32_t lds_op) {
-        // instruction t (q = wave + 4 t) fills k-rows 2 q, 2 q + 1; lane -> k-row 2 q + lane / 32,
-        // slot lane % 32; the swizzle term (k-row & 3) does not depend on t
+        // instruction t (q = wave + NW t) fills k-rows 2 q, 2 q + 1; lane -> k-row 2 q + lane / 32,
+        // slot lane % 32; the swizzle term (k-row & 3) does not depend on t (NW is even)
         const uint32_t r0 = 2u * wave + (lane >> 5);
         const uint32_t cl = (lane & 31u) ^ (4u * (r0 & 3u));
         src = reinterpret_cast<const char *>(p) + ((size_t)r0 * ld * 2u + mn0 * 2u + cl * 16u);
-        step = 8u * ld * 2u;
+        step = 2u * NW * ld * 2u;
         kstep = 64u * ld * 2u;
         const uint32_t grp = lane >> 4, s = lane & 15u;
         const uint32_t row = 8u * (grp >> 1) + (s >> 2);
-        const uint32_t col = wbase + 16u * (grp & 1u) + 4u * (s & 3u);   // wbase % 128 == 0
+        const uint32_t col = wbase + 16u * (grp & 1u) + 4u * (s & 3u);   // wbase % (32 NF) == 0
         const uint32_t rel = row * 512u + (((col >> 3) ^ (4u * (row & 3u))) * 16u) + (col & 7u) * 2u;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) lds[i] = lds_op + (rel ^ (64u * i));
+        for (int i = 0; i < NF; ++i) lds[i] = lds_op + (rel ^ (64u * i));
     }
     __device__ __forceinline__ void issue(int kt, lds_char *dst) const {
         const char *s = src + (uint32_t)kt * kstep;
 #pragma unroll
-        for (int t = 0; t < Dma256::IPO; ++t) dma16(s + t * step, dst + t * 4096u);
+        for (int t = 0; t < IPO; ++t) dma16(s + t * step, dst + t * (NW * 1024u));
     }
     // k-rows 16 ks + 4 h (+ 8): offsets 8192 ks + 2048 h keep the swizzle (multiples of 4 rows)
     __device__ __forceinline__ void read(Frag &f, uint32_t stage_off, int ks) const {
-#define SKL_TR2(I)                                                              \
-        ds_read8_tr<0>(f.v[I][0], lds[I] + stage_off + 8192u * ks);            \
-        ds_read8_tr<2048>(f.v[I][1], lds[I] + stage_off + 8192u * ks);
-        SKL_TR2(0) SKL_TR2(1) SKL_TR2(2) SKL_TR2(3)
-#undef SKL_TR2
+#pragma unroll
+        for (int i = 0; i < NF; ++i) {
+            ds_read8_tr<0>(f.v[i][0], lds[i] + stage_off + 8192u * ks);
+            ds_read8_tr<2048>(f.v[i][1], lds[i] + stage_off + 8192u * ks);
+        }
     }
     __device__ __forceinline__ static u32x4 op(const Frag &f, int i) {
         return u32x4{f.v[i][0].x, f.v[i][0].y, f.v[i][1].x, f.v[i][1].y};
     }
+    __device__ __forceinline__ static void pin_all(Frag &f) {
+#pragma unroll
+        for (int i = 0; i < NF; ++i) {
+            pin(f.v[i][0]);
+            pin(f.v[i][1]);
+        }
+    }
 };
 
-// lgkmcnt(N) that also claims to rewrite the fragments it guards, so every
-// MFMA reading them is ordered after the wait by data dependence (a bare
-// s_waitcnt builtin orders memory operations, not the pure MFMAs).
-template <int N> __device__ __forceinline__ void wait_frags(OpK::Frag &a, OpK::Frag &b) {
-    asm volatile("s_waitcnt lgkmcnt(%8)"
-                 : "+v"(a.v[0]), "+v"(a.v[1]), "+v"(a.v[2]), "+v"(a.v[3]), "+v"(b.v[0]), "+v"(b.v[1]),
-                   "+v"(b.v[2]), "+v"(b.v[3])
-                 : "i"(N));
-}
-template <int N> __device__ __forceinline__ void wait_frags(OpK::Frag &a, OpN::Frag &b) {
-    asm volatile("s_waitcnt lgkmcnt(%12)"
-                 : "+v"(a.v[0]), "+v"(a.v[1]), "+v"(a.v[2]), "+v"(a.v[3]), "+v"(b.v[0][0]), "+v"(b.v[0][1]),
-                   "+v"(b.v[1][0]), "+v"(b.v[1][1]), "+v"(b.v[2][0]), "+v"(b.v[2][1]), "+v"(b.v[3][0]),
-                   "+v"(b.v[3][1])
-                 : "i"(N));
-}
-template <int N> __device__ __forceinline__ void wait_frags(OpN::Frag &a, OpN::Frag &b) {
-    asm volatile("s_waitcnt lgkmcnt(%16)"
-                 : "+v"(a.v[0][0]), "+v"(a.v[0][1]), "+v"(a.v[1][0]), "+v"(a.v[1][1]), "+v"(a.v[2][0]),
-                   "+v"(a.v[2][1]), "+v"(a.v[3][0]), "+v"(a.v[3][1]), "+v"(b.v[0][0]), "+v"(b.v[0][1]),
-                   "+v"(b.v[1][0]), "+v"(b.v[1][1]), "+v"(b.v[2][0]), "+v"(b.v[2][1]), "+v"(b.v[3][0]),
-                   "+v"(b.v[3][1])
-                 : "i"(N));
-}
+template <bool KC, int NW, int NF> struct DmaOpSel { typedef OpK<NW, NF> type; };
+template <int NW, int NF> struct DmaOpSel<false, NW, NF> { typedef OpN<NW, NF> type; };
 
-template <bool KC> struct DmaOpSel { typedef OpK type; };
-template <> struct DmaOpSel<false> { typedef OpN type; };
-
-template <class Epi, bool A_KC, bool B_KC>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+template <class Epi, bool A_KC, bool B_KC, int NW>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4)))
     gemm_dma_kernel(GemmShape sh, const half_t *__restrict__ A, const half_t *__restrict__ B,
                     typename Epi::Params ep) {
-    typedef Dma256 C;
-    typedef typename DmaOpSel<A_KC>::type OA;
-    typedef typename DmaOpSel<B_KC>::type OB;
+    typedef DmaCfg<NW> C;
+    typedef typename DmaOpSel<A_KC, NW, C::MT>::type OA;
+    typedef typename DmaOpSel<B_KC, NW, C::NTL>::type OB;
     // a fragment set may be consumed while at most the other set's reads are pending
     constexpr int SET_READS = OA::READS + OB::READS;
     constexpr int WAIT_SET = SET_READS < 15 ? SET_READS : 15;
@@ -255,9 +256,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
         oa.read(fa[set], stage * C::STAGEB, ks);
         ob.read(fb[set], stage * C::STAGEB, ks);
     };
-    static_assert(C::MT == 4 && C::NTL == 4, "operand reads are written out for 4 x 4 fragments");
     auto mma = [&](int set) {
-        wait_frags<WAIT_SET>(fa[set], fb[set]);
+        asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(WAIT_SET));
+        OA::pin_all(fa[set]);
+        OB::pin_all(fb[set]);
 #pragma unroll
         for (int i = 0; i < C::MT; ++i)
 #pragma unroll
@@ -299,11 +301,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
     // i = pass * MTP + ii of both wave rows).  A thread owns the fixed 4-column
     // group c of the tile (a wave covers one whole 256-column row per step, so
     // LDS reads and global accesses are contiguous) and walks rows
-    // wave, wave + 4, ...; the per-element loads of EPI_BATCH rows are issued
+    // wave, wave + NW, ...; the per-element loads of EPI_BATCH rows are issued
     // before any of them is consumed, so the loop keeps that many in flight
-    // instead of paying one memory latency per row.
-    constexpr int EPI_BATCH = 8;
-    constexpr int ROWS_PER_THREAD = PROWS / C::NWAVES;   // 32 per pass
+    // instead of paying one memory latency per row (4 rows for large per-row
+    // operand sets at 8 waves, whose 256-register budget they would overflow).
+    constexpr int EPI_BATCH = (NW == 8 && sizeof(typename Epi::Pre) > 32) ? 4 : 8;
+    constexpr int ROWS_PER_THREAD = PROWS / NW;
     static_assert(ROWS_PER_THREAD % EPI_BATCH == 0, "epilogue batch");
     static_assert(C::BN / 4 == 64, "one wave per 256-column row");
     float *E = reinterpret_cast<float *>(smem);
@@ -333,14 +336,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))
 #pragma unroll
             for (int u = 0; u < EPI_BATCH; ++u) {
                 // E row r holds tile row wmi * TWM + pass * MTP * 32 + rr
-                const uint32_t r = wave + (uint32_t)C::NWAVES * (b + u);
+                const uint32_t r = wave + (uint32_t)NW * (b + u);
                 const uint32_t wmi = r / (MTP * 32), rr = r % (MTP * 32);
                 mrow[u] = m0 + wmi * C::TWM + pass * MTP * 32 + rr;
                 Epi::load(ep, (uint64_t)mrow[u] * Epi::ldc(ep) + n0 + c, mrow[u], pre[u]);
             }
 #pragma unroll
             for (int u = 0; u < EPI_BATCH; ++u) {
-                const uint32_t r = wave + (uint32_t)C::NWAVES * (b + u);
+                const uint32_t r = wave + (uint32_t)NW * (b + u);
                 const floatx4 v = *reinterpret_cast<const floatx4 *>(E + r * EPITCH + c);
                 Epi::finish(ep, (uint64_t)mrow[u] * Epi::ldc(ep) + n0 + c, mrow[u], n0 + c, v, col, pre[u]);
             }

@@ -103,8 +103,14 @@ struct ErrArgs {
     float *grad, *d_prenorm, *d_norm_w, *d_norm_b;
     half_t *d_prenorm_h;
 };
-hipError_t launch_output_error(const ErrArgs &a, hipStream_t s);
-hipError_t launch_error_from_sum(const ErrArgs &a, hipStream_t s);
+// Both also write the column sums of d_prenorm / dNorm_w / dNorm_b over the
+// rows into partials [splits x 3 x n] when partials is non-null and the
+// vectorised kernel applies (n % 4 == 0, 16-byte aligned buffers); *sums
+// tells whether they did.
+hipError_t launch_output_error(const ErrArgs &a, float *partials, uint32_t splits, bool *sums, hipStream_t s);
+hipError_t launch_error_from_sum(const ErrArgs &a, float *partials, uint32_t splits, bool *sums, hipStream_t s);
+// Row splits the error kernels use for their column sums.
+uint32_t err_col_splits(uint32_t rows, uint32_t n);
 
 // Column sums of up to three fp32 [rows x n] arrays into partials
 // [splits x 3 x n]; then the bias / norm-parameter optimiser.

@@ -180,7 +180,8 @@ def test_error_from_sum_and_input_grad(ctx, half, M, K, N, norm, act):
 # ---------------------------------------------------------------------------------------------
 # backward: dW / db / norm sums + optimiser
 # ---------------------------------------------------------------------------------------------
-def _run_backward(ctx, half, M, K, N, norm, opt_kind, step=1, regularisation=0, regu_coeff=0.0, lr=0.01):
+def _run_backward(ctx, half, M, K, N, norm, opt_kind, step=1, regularisation=0, regu_coeff=0.0, lr=0.01,
+                  call_between=False):
     ob, db = make_pair(ctx, K, N, M, seed=41 + M, half=half, norm=norm, act=abi.ACT_SILU,
                        regularisation=regularisation, regu_coeff=regu_coeff)
     x = inputs(42, M, K, half)
@@ -189,6 +190,10 @@ def _run_backward(ctx, half, M, K, N, norm, opt_kind, step=1, regularisation=0, 
     s = (rng(43).standard_normal((M, N)) * 512).astype(np.float32)
     ob.error_from_sum(s, M)
     db.error_from_sum(torch.from_numpy(s).cuda(), M)
+    if call_between:
+        # any entry point between the error and the backward call: the backward then sums
+        # d_prenorm / dNorm over the rows itself instead of using the error call's sums
+        ctx.synchronize()
     if opt_kind == abi.OPT_SGD:
         oo, do = O.Optimiser.sgd(0.0), abi.sgd(0.0)
     else:
@@ -217,6 +222,40 @@ def test_backward_sgd(ctx, half, M, K, N, norm):
         check("dv_norm_b", db.get("dv_norm_b"), ob.dv_norm_b, tol)
     if half:
         assert np.array_equal(db.get("w"), f16(db.get("master_w"))), "w must equal f16(master_w)"
+
+
+@pytest.mark.parametrize("half", [False, True])
+@pytest.mark.parametrize("norm", [0, 1, 2])
+@pytest.mark.parametrize("call_between", [False, True])
+def test_backward_column_sums_from_error_call_or_recomputed(ctx, half, norm, call_between):
+    """db and the dNorm sums come from the error call's own pass over the rows when the
+    backward directly follows it, and are recomputed otherwise; both match the oracle."""
+    ob, db = _run_backward(ctx, half, 320, 96, 200, norm, abi.OPT_SGD, call_between=call_between)
+    tol = FP16_TOL if half else FP32_TOL
+    check("dv_b (= db)", db.get("dv_b"), ob.dv_b, tol)
+    if norm:
+        check("dv_norm_w", db.get("dv_norm_w"), ob.dv_norm_w, tol)
+    if norm > 1:
+        check("dv_norm_b", db.get("dv_norm_b"), ob.dv_norm_b, tol)
+
+
+def test_backward_column_sums_not_taken_from_another_block(ctx):
+    """Error calls on blocks A then B, backward on A: A's bias gradient must come from A's
+    own d_prenorm, not from the column sums B's error call left behind."""
+    M, K, N = 192, 64, 128
+    oa, da = make_pair(ctx, K, N, M, seed=61, act=abi.ACT_SILU)
+    ob_, db_ = make_pair(ctx, K, N, M, seed=62, act=abi.ACT_SILU)
+    x = inputs(63, M, K, False)
+    for o, d, sd in ((oa, da, 64), (ob_, db_, 65)):
+        o.forward(x, M)
+        d.forward(dev(x, False), M)
+        s = (rng(sd).standard_normal((M, N)) * 512).astype(np.float32)
+        o.error_from_sum(s, M)
+        d.error_from_sum(torch.from_numpy(s).cuda(), M)
+    oa.backward(x, O.Optimiser.sgd(0.0), O.Optimiser.sgd(0.0), M, 0.01, 3.4e38, 1)
+    da.backward(dev(x, False), abi.train_ctx(abi.sgd(0.0), abi.sgd(0.0), M, 0.01), 1)
+    torch.cuda.synchronize()
+    check("dv_b (= db of block A)", da.get("dv_b"), oa.dv_b, FP32_TOL)
 
 
 @pytest.mark.parametrize("half", [False, True])

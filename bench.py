@@ -1,15 +1,22 @@
-"""Headline benchmark: fp16 DenseBlock fwd+bwd+Adam at B=8192, 4096->4096 on one MI355X.
+"""DenseBlock hot-path benchmark on one MI355X (default: the headline).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3|c2] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3|c2|c4|c5] [--no-cpu]
     python bench.py --copy-probe MIB      (counter calibration copy only)
 
-One step = one pass of the DenseBlock hot path over one batch, all through the
-C ABI (libsoklyn_hip.so), inputs resident in HBM:
-  1. skl_dense_forward        Z = X.W + b, SiLU          (GEMM, fused epilogue)
-  2. skl_dense_error_from_sum dP = dY * SiLU'(Z)          (element-wise)
-  3. skl_dense_backward       dW = X^T.dP + Adam on W, db + Adam on b
+Every step goes through the C ABI (libsoklyn_hip.so) with its inputs resident in HBM.
+
+Single blocks (c3 = BASELINE config 3, the headline; c2 = config 2), one step =
+  1. skl_dense_forward        Z = X.W + b, act           (GEMM, fused epilogue)
+  2. skl_dense_error_from_sum dP = dY * act'(Z)           (element-wise + column sums)
+  3. skl_dense_backward       dW = X^T.dP + optimiser on W, db + optimiser on b
   4. skl_dense_input_grad     dX = dP.W^T (updated W, src/ffn.rs:142-163 order)
-Algorithmic work = 3 GEMMs x 2*M*K*N flops.  Prints one JSON line.
+  algorithmic work = 3 GEMMs x 2*M*K*N flops.
+MLPs (c4 = config 4, c5 = config 5), one step = FeedForwardNetwork's train step
+(src/ffn.rs:40-166): forward of every layer, output error, backward of the output
+layer, then for each lower layer the hidden error from the updated layer above
+followed by its own backward;
+  algorithmic work = forward and dW of every layer + dX of layers 2..L.
+Prints one JSON line.
 """
 from __future__ import annotations
 
@@ -25,12 +32,35 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK = {"f16": 2516.6, "f32": 157.3}   # dense MFMA TFLOP/s: 256 CU x 2.4 GHz x {4096, 256} flop/clk/CU
+HEADLINE = "DenseBlock fwd+bwd TFLOP/s & % MFMA peak (fp16, B=8192, 4096→4096)"
+
+# activation / norm / loss / optimiser codes (reference ordinals, src/util/function.rs)
+ACT_RELU, ACT_LEAKY, ACT_SIGMOID, ACT_SOFTMAX, ACT_SILU, ACT_MISH, ACT_IDENTITY = 2, 3, 1, 5, 6, 7, 0
+NORM_RMS, NORM_LAYER = 1, 2
+LOSS_CE, LOSS_BCE = 1, 2
+
 CONFIGS = {
-    # BASELINE.json configs[2] (headline) and configs[1]
-    "c3": dict(M=8192, K=4096, N=4096, half=True, act=6, workload="DenseBlock fp16 mixed precision, "
-               "X[8192x4096] f16, W[4096x4096] f16 copy of fp32 He-normal master, SiLU, fwd+bwd(dX,dW)+Adam"),
-    "c2": dict(M=4096, K=1024, N=1024, half=False, act=2, workload="DenseBlock fp32, X[4096x1024], "
-               "W[1024x1024] He-normal, ReLU, fwd+bwd(dX,dW,db)+SGD"),
+    # BASELINE.json configs[2] (headline) and configs[1]: single DenseBlocks
+    "c3": dict(kind="block", M=8192, K=4096, N=4096, half=True, act=ACT_SILU,
+               metric=HEADLINE,
+               workload="DenseBlock fp16 mixed precision, X[8192x4096] f16, W[4096x4096] f16 copy of fp32 "
+                        "He-normal master, SiLU, fwd+bwd(dX,dW)+Adam"),
+    "c2": dict(kind="block", M=4096, K=1024, N=1024, half=False, act=ACT_RELU,
+               metric="DenseBlock fwd+bwd TFLOP/s & % MFMA peak (fp32, B=4096, 1024→1024)",
+               workload="DenseBlock fp32, X[4096x1024], W[1024x1024] He-normal, ReLU, fwd+bwd(dX,dW,db)+SGD"),
+    # multi-layer train steps
+    "c4": dict(kind="mlp", M=16384, dims=[3072, 2048, 2048, 2048, 2048, 10], x="uniform",
+               hidden=dict(norm=NORM_RMS, act=ACT_MISH, mask_coeff=0.1), dropout=True,
+               loss=LOSS_CE, loss_act=ACT_SOFTMAX, timed_layer=1,
+               metric="MLP train step TFLOP/s & % MFMA peak (fp16, B=16384, 3072→2048⁴→10)",
+               workload="5-layer MLP 3072->2048->2048->2048->2048->10 fp16 mixed precision, batch 16384, "
+                        "RMSNorm + Mish + dropout 0.1 hidden, softmax CE, Adam; fwd+bwd+Adam train step"),
+    "c5": dict(kind="mlp", M=12345, dims=[777, 1531, 3001, 13], x="normal2",
+               hidden=dict(norm=NORM_LAYER, act=ACT_LEAKY, leaky=0.01), dropout=False,
+               loss=LOSS_BCE, loss_act=ACT_SIGMOID, timed_layer=0,
+               metric="MLP train step TFLOP/s & % MFMA peak (fp16, B=12345, 777→1531→3001→13)",
+               workload="Ragged MLP 777->1531->3001->13 fp16 mixed precision, batch 12345, LayerNorm + "
+                        "LeakyReLU(0.01) hidden, sigmoid BCE, Adam; fwd+bwd+Adam train step"),
 }
 
 
@@ -73,7 +103,42 @@ def traffic_record(config: str, kernel: str):
     return rec
 
 
-def cpu_baseline(cfg, rows: int, reps: int = 3):
+def mlp_flops(dims, M):
+    """Forward and dW of every layer + dX of layers 2..L (the reference never forms dX
+    of the network input)."""
+    layer = [2.0 * M * dims[i] * dims[i + 1] for i in range(len(dims) - 1)]
+    return 2 * sum(layer) + sum(layer[1:])
+
+
+def mlp_inputs(cfg, g, rows):
+    d0, d_last = cfg["dims"][0], cfg["dims"][-1]
+    if cfg["x"] == "uniform":
+        x = g.random((rows, d0), dtype=np.float32)
+    else:                                   # N(0, 2): variance 2
+        x = g.standard_normal((rows, d0)).astype(np.float32) * np.float32(np.sqrt(2.0))
+    x = x.astype(np.float16).astype(np.float32)
+    if cfg["loss"] == LOSS_CE:
+        t = np.zeros((rows, d_last), np.float32)
+        t[np.arange(rows), g.integers(0, d_last, rows)] = 1.0
+    else:
+        t = (g.random((rows, d_last)) > 0.5).astype(np.float32)
+    return x, t
+
+
+def mlp_weights(cfg, g):
+    dims = cfg["dims"]
+    return [(g.standard_normal((dims[i], dims[i + 1])) * np.sqrt(2.0 / dims[i])).astype(np.float32)
+            for i in range(len(dims) - 1)]
+
+
+def dropout_seeds(cfg, step):
+    # weight ids of an fp16 training network built in order: 27 tensors per block (src/mlp.rs:45-421)
+    from soklyn_amd import abi
+    return [int(abi.load().skl_scramble_seed(step, 27 * i)) if cfg["dropout"] else 0
+            for i in range(len(cfg["dims"]) - 1)]
+
+
+def cpu_baseline_block(cfg, rows: int, reps: int = 3):
     """The oracle (C restatement, fp32, OpenMP over the host cores) on the same step:
     one warm-up pass, then the median of `reps` timed passes."""
     from oracle import oracle as O
@@ -102,6 +167,131 @@ def cpu_baseline(cfg, rows: int, reps: int = 3):
                       f"on the oracle; median of {reps} passes after one warm-up, {dt:.2f} s per pass"}
 
 
+def cpu_baseline_mlp(cfg, rows: int, reps: int = 3):
+    """The oracle's FeedForwardNetwork train step (fp32) on `rows` of the batch."""
+    from oracle import oracle as O
+    g = np.random.default_rng(0)
+    dims = cfg["dims"]
+    ws = mlp_weights(cfg, g)
+    x, t = mlp_inputs(cfg, g, rows)
+    L = len(dims) - 1
+    obs = [O.OracleBlock(dims[i], dims[i + 1], rows, ws[i], **(cfg["hidden"] if i < L - 1 else
+                                                                dict(act=ACT_IDENTITY))) for i in range(L)]
+    opt = O.Optimiser.adam()
+
+    def one(step):
+        seeds = dropout_seeds(cfg, step)
+        t0 = time.perf_counter()
+        cur, outs = x, []
+        for ob, sd in zip(obs, seeds):
+            cur = ob.forward(cur, rows, cfg["dropout"], sd)
+            outs.append(cur)
+        obs[L - 1].output_error(t, cfg["loss"], cfg["loss_act"])
+        obs[L - 1].backward(outs[L - 2], opt, opt, rows, 1e-3, 3.4e38, step)
+        for i in range(L - 2, -1, -1):
+            obs[i].hidden_error(obs[i + 1], rows)
+            obs[i].backward(outs[i - 1] if i > 0 else x, opt, opt, rows, 1e-3, 3.4e38, step)
+        return time.perf_counter() - t0
+
+    one(1)
+    times = sorted(one(2 + i) for i in range(reps))
+    dt = times[len(times) // 2]
+    return {"value": round(mlp_flops(dims, rows) / dt / 1e12, 6), "unit": "TFLOP/s", "cores": O.num_threads(),
+            "kind": "port",
+            "sample": f"{rows} of {cfg['M']} batch rows of the same train step (all layers fwd, loss, bwd + Adam) "
+                      f"in fp32 on the oracle; median of {reps} passes after one warm-up, {dt:.2f} s per pass"}
+
+
+class BlockBench:
+    """Single DenseBlock: forward -> error_from_sum -> backward -> input_grad."""
+    calls = ("forward_gemm", "error_elementwise", "dw_gemm_adam", "dx_gemm")
+    single_launch = ("forward_gemm", "dx_gemm")   # one GEMM kernel per call at these shapes
+
+    def __init__(self, cfg, ctx, stream):
+        import torch
+        from soklyn_amd import abi
+        from soklyn_amd.devblock import DeviceBlock
+        M, K, N, half = cfg["M"], cfg["K"], cfg["N"], cfg["half"]
+        dt = torch.float16 if half else torch.float32
+        g = np.random.default_rng(1)
+        w = (g.standard_normal((K, N)) * np.sqrt(2.0 / K)).astype(np.float32)
+        self.blk = DeviceBlock(ctx, K, N, M, w, half=half, act=cfg["act"], master_w=w if half else None,
+                               b=(g.standard_normal((1, N)) * 0.01).astype(np.float32))
+        self.x = torch.randn((M, K), device="cuda", dtype=torch.float32).to(dt)
+        self.dy = torch.randn((M, N), device="cuda", dtype=torch.float32) * 512.0
+        self.dx = torch.empty((M, K), device="cuda", dtype=torch.float32)
+        opt = abi.adam(0.9, 0.999, 1e-8) if half else abi.sgd(0.0)
+        self.tc = abi.train_ctx(opt, opt, M, 1e-3 if half else 1e-2)
+        self.M = M
+        self.step_no = 0
+        self.flops = 3 * 2.0 * M * K * N
+        self.kernel_flops = {"forward_gemm": 2.0 * M * K * N, "dx_gemm": 2.0 * M * K * N}
+        self.stream = stream
+
+    def step(self, ev=None):
+        # ev: per-call (start, end) HIP events on the launch stream, recorded inside the
+        # timed steps so each call is timed in the step's own context
+        self.step_no += 1
+        b, M = self.blk, self.M
+        fns = (lambda: b.forward(self.x, M), lambda: b.error_from_sum(self.dy, M),
+               lambda: b.backward(self.x, self.tc, self.step_no), lambda: b.input_grad(M, self.dx))
+        for i, fn in enumerate(fns):
+            if ev is not None:
+                ev[i][0].record(self.stream)
+            fn()
+            if ev is not None:
+                ev[i][1].record(self.stream)
+
+
+class MlpBench:
+    """FeedForwardNetwork train step over DeviceBlocks (src/ffn.rs:40-166 order)."""
+
+    def __init__(self, cfg, ctx, stream):
+        import torch
+        from soklyn_amd import abi
+        from soklyn_amd.devblock import DeviceBlock
+        self.cfg, self.abi, self.stream = cfg, abi, stream
+        dims, M = cfg["dims"], cfg["M"]
+        g = np.random.default_rng(1)
+        ws = mlp_weights(cfg, g)
+        L = len(dims) - 1
+        self.blocks = [DeviceBlock(ctx, dims[i], dims[i + 1], M, ws[i], half=True, master_w=ws[i],
+                                   **(cfg["hidden"] if i < L - 1 else dict(act=ACT_IDENTITY)))
+                       for i in range(L)]
+        x, t = mlp_inputs(cfg, g, M)
+        self.x = torch.from_numpy(x).cuda().half()
+        self.t = torch.from_numpy(t).cuda().half()
+        self.tc = abi.train_ctx(abi.adam(), abi.adam(), M, 1e-3)
+        self.M, self.L = M, L
+        self.step_no = 0
+        self.flops = mlp_flops(dims, M)
+        # the roofline call: the hidden error of layer `timed_layer` (one GEMM launch with the
+        # act' / mask / norm-gradient epilogue), dX through the weights of the layer above it
+        k = cfg["timed_layer"]
+        self.timed = f"hidden_error_gemm_layer{k}"
+        self.calls = (self.timed,)
+        self.single_launch = (self.timed,)
+        self.kernel_flops = {self.timed: 2.0 * M * dims[k + 1] * dims[k + 2]}
+
+    def step(self, ev=None):
+        self.step_no += 1
+        cfg, b, M, L = self.cfg, self.blocks, self.M, self.L
+        seeds = dropout_seeds(cfg, self.step_no)
+        cur = self.x
+        for blk, sd in zip(b, seeds):
+            cur = blk.forward(cur, M, cfg["dropout"], sd)
+        b[L - 1].output_error(self.t, cfg["loss"], cfg["loss_act"])
+        b[L - 1].backward(b[L - 2].out, self.tc, self.step_no)
+        for i in range(L - 2, -1, -1):
+            timed = ev is not None and i == cfg["timed_layer"]
+            if timed:
+                ev[0][0].record(self.stream)
+            b[i].hidden_error(b[i + 1], M)
+            if timed:
+                ev[0][1].record(self.stream)
+            b[i].backward(b[i - 1].out if i > 0 else self.x, self.tc, self.step_no)
+
+
 def main():
     args = parse()
     if args.copy_probe:
@@ -113,46 +303,19 @@ def main():
         sys.exit(2)
     import torch
     from soklyn_amd import abi
-    from soklyn_amd.devblock import DeviceBlock
 
     cfg = CONFIGS[args.config]
-    M, K, N, half = cfg["M"], cfg["K"], cfg["N"], cfg["half"]
-    dt = torch.float16 if half else torch.float32
     torch.manual_seed(0)
     stream = torch.cuda.Stream()          # explicit, default priority (stream 0 has handle 0)
     torch.cuda.set_stream(stream)
     ctx = abi.Context(0, 16)
     ctx.set_stream(stream.cuda_stream)
     ctx.set_sync(False)
-
-    g = np.random.default_rng(1)
-    w = (g.standard_normal((K, N)) * np.sqrt(2.0 / K)).astype(np.float32)
-    blk = DeviceBlock(ctx, K, N, M, w, half=half, act=cfg["act"], master_w=w if half else None,
-                      b=(g.standard_normal((1, N)) * 0.01).astype(np.float32))
-    x = torch.randn((M, K), device="cuda", dtype=torch.float32).to(dt)
-    dy = torch.randn((M, N), device="cuda", dtype=torch.float32) * 512.0
-    dx = torch.empty((M, K), device="cuda", dtype=torch.float32)
-    opt = abi.adam(0.9, 0.999, 1e-8) if half else abi.sgd(0.0)
-    tc = abi.train_ctx(opt, opt, M, 1e-3 if half else 1e-2)
-    step_no = [0]
-
-    calls = ("forward_gemm", "error_elementwise", "dw_gemm_adam", "dx_gemm")
-
-    def step(ev=None):
-        # ev: per-call (start, end) HIP events on the launch stream, recorded
-        # inside the timed steps so each call is timed in the step's own context
-        step_no[0] += 1
-        fns = (lambda: blk.forward(x, M), lambda: blk.error_from_sum(dy, M),
-               lambda: blk.backward(x, tc, step_no[0]), lambda: blk.input_grad(M, dx))
-        for i, fn in enumerate(fns):
-            if ev is not None:
-                ev[i][0].record(stream)
-            fn()
-            if ev is not None:
-                ev[i][1].record(stream)
+    bench = BlockBench(cfg, ctx, stream) if cfg["kind"] == "block" else MlpBench(cfg, ctx, stream)
+    calls = bench.calls
 
     for _ in range(args.warmup):
-        step()
+        bench.step()
     torch.cuda.synchronize()
     evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in calls]
            for _ in range(args.steps)]
@@ -160,28 +323,32 @@ def main():
     t0 = time.perf_counter()
     ev0.record(stream)
     for k in range(args.steps):
-        step(evs[k])
+        bench.step(evs[k])
     ev1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms = ev0.elapsed_time(ev1) / args.steps
-    flops = 3 * 2.0 * M * K * N
-    value = flops / (ms * 1e-3) / 1e12
-    # average duration of each call over the timed steps (forward and dX are one
-    # kernel launch each at these shapes; dW+Adam adds the bias column sums)
+    value = bench.flops / (ms * 1e-3) / 1e12
+    # average duration of each timed call over the timed steps
     kern = {c: sum(evs[k][i][0].elapsed_time(evs[k][i][1]) for k in range(args.steps)) / args.steps
             for i, c in enumerate(calls)}
 
-    # The roofline kernel: the slower of the two single-launch GEMM calls (forward:
-    # Z = X.W with the fused bias + activation epilogue; dX = dP.W^T).
-    dom = max(("forward_gemm", "dx_gemm"), key=lambda k: kern[k])
-    gemm_flops = 2.0 * M * K * N
-    achieved = gemm_flops / (kern[dom] * 1e-3) / 1e12
+    # The roofline kernel: the slowest single-launch GEMM call
+    dom = max(bench.single_launch, key=lambda k: kern[k])
+    achieved = bench.kernel_flops[dom] / (kern[dom] * 1e-3) / 1e12
+    half = cfg.get("half", True)
     peak = PEAK["f16" if half else "f32"]
     trec = traffic_record(args.config, dom)
+    config = {"workload": cfg["workload"], "M": cfg["M"]}
+    if cfg["kind"] == "block":
+        config.update(K=cfg["K"], N=cfg["N"])
+    else:
+        config.update(dims=cfg["dims"])
+    config.update(gflop_per_step=round(bench.flops / 1e9, 3), pct_of_peak_step=round(100 * value / peak, 2),
+                  wall_s=round(wall, 3))
 
     out = {
-        "metric": "DenseBlock fwd+bwd TFLOP/s & % MFMA peak (fp16, B=8192, 4096→4096)",
+        "metric": cfg["metric"],
         "value": round(value, 2),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -192,9 +359,9 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f16" if half else "f32",
-        "data": "synthetic (seeded N(0,1) inputs, He-normal weights, N(0,1)*512 upstream gradient)",
-        "config": {"workload": cfg["workload"], "M": M, "K": K, "N": N,
-                   "pct_of_peak_step": round(100 * value / peak, 2), "wall_s": round(wall, 3)},
+        "data": "synthetic (seeded inputs and targets of the config's distributions, He-normal weights"
+                + (", N(0,1)*512 upstream gradient)" if cfg["kind"] == "block" else ")"),
+        "config": config,
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(achieved / peak, 4),
                      "traffic": trec["bytes_per_launch"] if trec else None,
@@ -202,9 +369,11 @@ def main():
                      "kernel_ms": {k: round(v, 4) for k, v in kern.items()}},
     }
     if not args.no_cpu:
-        # the whole batch: about 10-20 s of the oracle on the host cores
-        rows = args.cpu_rows or M
-        out["cpu_baseline"] = cpu_baseline(cfg, rows)
+        if cfg["kind"] == "block":
+            out["cpu_baseline"] = cpu_baseline_block(cfg, args.cpu_rows or cfg["M"])
+        else:
+            # a quarter of the batch: 10-20 s of the oracle on the host cores
+            out["cpu_baseline"] = cpu_baseline_mlp(cfg, args.cpu_rows or cfg["M"] // 4)
     print(json.dumps(out), flush=True)
     ctx.close()
 

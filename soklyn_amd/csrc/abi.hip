@@ -117,13 +117,157 @@ size_t elem_size(uint32_t dtype) { return dtype == SKL_F16 ? 2 : 4; }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Large fp16 GEMMs whose operands are not k-contiguous run on transposed
-// copies (workspace) instead: one HBM pass per operand buys the faster
-// k-contiguous MFMA staging.  Shapes must allow 16-byte chunks everywhere.
-bool use_transposed_operands(uint32_t dtype, uint32_t M, uint32_t N, uint32_t K, uint32_t ld) {
-    if (dtype != SKL_F16) return false;
-    if ((M | N | K | ld) & 7u) return false;
-    return gemm_large_tile(dtype, M, N);
+// ---- GEMM planning ------------------------------------------------------------------
+// Every DenseBlock GEMM runs on the fastest path its shapes allow:
+//  * the 256x256 direct-to-LDS kernel (fp16).  Operands it cannot read as
+//    stored (M, N not whole 256 tiles, K not a multiple of 128, rows not
+//    16-byte aligned) are first copied into the workspace zero-padded to those
+//    multiples, and the epilogue stops at the real M x N.  Used when the padded
+//    output wastes at most half of its grid and there are at least 192 tiles,
+//    counting the split-K slices a dW with fewer tiles than CUs is given (their
+//    fp32 partial sums, in the workspace, are reduced by the optimiser kernel).
+//  * the register-staged kernels otherwise (fp32; small or skinny fp16), with
+//    the same split-K for small dW grids.
+struct GemmPlan {
+    bool dma;
+    bool pad_a, pad_b;
+    uint32_t Mp, Np, Kp;       // dims the kernel runs on
+    uint32_t splits;           // split-K slices of a dW (then DwPartial + reduce)
+    size_t a_bytes, b_bytes, part_bytes;
+    size_t bytes() const { return a_bytes + b_bytes + part_bytes; }
+};
+
+uint32_t round_up(uint32_t v, uint32_t m) { return (v + m - 1) / m * m; }
+
+// A stored operand the DMA kernel can read in place: rows x cols (k-contiguous:
+// rows = m or n, cols = k; else rows = k, cols = m or n) with whole tiles.
+bool dma_operand_ok(const void *p, uint32_t rows, uint32_t cols, uint32_t ld, uint32_t rows_mult,
+                    uint32_t cols_mult) {
+    return rows % rows_mult == 0 && cols % cols_mult == 0 && ld % 8 == 0 && aligned16(p);
+}
+
+GemmPlan plan_gemm(const GemmLaunch &g) {
+    GemmPlan p{};
+    p.splits = 1;
+    p.Mp = g.M;
+    p.Np = g.N;
+    p.Kp = g.K;
+    const bool dw = g.op == Op::DwOpt;
+    if (g.dtype == SKL_F16 && gemm_dma_enabled() && g.M && g.N && g.K) {
+        const uint32_t Mp = round_up(g.M, 256), Np = round_up(g.N, 256), Kp = round_up(g.K, 128);
+        const uint32_t tiles = (Mp / 256) * (Np / 256);
+        uint32_t splits = 1;
+        if (dw && tiles < 160) {
+            splits = (256 + tiles - 1) / tiles;
+            if (splits > Kp / 512) splits = Kp / 512;   // slices of at least 512 k
+            if (splits > 16) splits = 16;
+            if (splits < 1) splits = 1;
+            splits = gemm_dma_splits(Kp, splits);
+        }
+        const bool waste_ok = (uint64_t)Mp * Np <= (uint64_t)g.M * g.N * 3 / 2;
+        // the kernel's operand offsets are 32-bit
+        const uint64_t a_span = g.a_kcontig ? (uint64_t)Mp * (g.lda > Kp ? g.lda : Kp)
+                                            : (uint64_t)Kp * (g.lda > Mp ? g.lda : Mp);
+        const uint64_t b_span = g.b_kcontig ? (uint64_t)Np * (g.ldb > Kp ? g.ldb : Kp)
+                                            : (uint64_t)Kp * (g.ldb > Np ? g.ldb : Np);
+        const bool offsets_ok = a_span * 2 < (1ull << 32) && b_span * 2 < (1ull << 32);
+        if (waste_ok && offsets_ok && tiles * splits >= 192) {
+            p.dma = true;
+            p.Mp = Mp;
+            p.Np = Np;
+            p.Kp = Kp;
+            p.splits = splits;
+            // A: k-contiguous [M x K] or m-contiguous [K x M]; B likewise with N
+            p.pad_a = g.a_kcontig ? !dma_operand_ok(g.A, g.M, g.K, g.lda, 256, 128)
+                                  : !dma_operand_ok(g.A, g.K, g.M, g.lda, 128, 256);
+            p.pad_b = g.b_kcontig ? !dma_operand_ok(g.B, g.N, g.K, g.ldb, 256, 128)
+                                  : !dma_operand_ok(g.B, g.K, g.N, g.ldb, 128, 256);
+            // 256-byte aligned regions
+            p.a_bytes = p.pad_a ? ((size_t)Mp * Kp * 2 + 255) & ~(size_t)255 : 0;
+            p.b_bytes = p.pad_b ? ((size_t)Np * Kp * 2 + 255) & ~(size_t)255 : 0;
+            p.part_bytes = splits > 1 ? (size_t)splits * Mp * Np * sizeof(float) : 0;
+            return p;
+        }
+    }
+    // register-staged kernels; split-K for small dW grids
+    if (dw) {
+        const uint32_t tiles = gemm_tiles(g.dtype, g.M, g.N);
+        const uint32_t bk = gemm_bk(g.dtype);
+        if (tiles < 160 && g.K >= 8 * bk) {
+            uint32_t splits = (256 + tiles - 1) / tiles;
+            const uint32_t max_splits = g.K / (4 * bk);
+            if (splits > max_splits) splits = max_splits;
+            if (splits > 16) splits = 16;
+            if (splits >= 2) {
+                p.splits = splits;
+                p.part_bytes = (size_t)splits * g.M * g.N * sizeof(float);
+            }
+        }
+    }
+    return p;
+}
+
+// Runs g as planned; ws holds plan.bytes() of workspace.
+int32_t exec_gemm(skl_ctx *ctx, GemmLaunch g, const GemmPlan &p, char *ws) {
+    char *wa = ws, *wb = ws + p.a_bytes, *wpart = ws + p.a_bytes + p.b_bytes;
+    const OptEpi oe = g.opt;
+    const uint32_t M = g.M, N = g.N;
+    if (p.dma) {
+        if (p.pad_a) {
+            if (g.a_kcontig)
+                SKL_TRY(launch_pad_h(g.A, g.M, g.K, g.lda, wa, p.Mp, p.Kp, ctx->stream));
+            else
+                SKL_TRY(launch_pad_h(g.A, g.K, g.M, g.lda, wa, p.Kp, p.Mp, ctx->stream));
+            g.A = wa;
+            g.lda = g.a_kcontig ? p.Kp : p.Mp;
+        }
+        if (p.pad_b) {
+            if (g.b_kcontig)
+                SKL_TRY(launch_pad_h(g.B, g.N, g.K, g.ldb, wb, p.Np, p.Kp, ctx->stream));
+            else
+                SKL_TRY(launch_pad_h(g.B, g.K, g.N, g.ldb, wb, p.Kp, p.Np, ctx->stream));
+            g.B = wb;
+            g.ldb = g.b_kcontig ? p.Kp : p.Np;
+        }
+        g.mv = M;
+        g.nv = N;
+        g.M = p.Mp;
+        g.N = p.Np;
+        g.K = p.Kp;
+        if (p.splits > 1) {
+            // fp32 partial planes on the padded grid; the optimiser kernel adds them up
+            g.op = Op::DwPartial;
+            g.splits = p.splits;
+            g.st.out = reinterpret_cast<float *>(wpart);
+            g.st.split_stride = (uint64_t)p.Mp * p.Np;
+            g.st.ldc = p.Np;
+            g.mv = g.M;
+            g.nv = g.N;
+        }
+        SKL_TRY(launch_gemm_dma(g, ctx->stream));
+    } else {
+        if (p.splits > 1) {
+            g.op = Op::DwPartial;
+            g.splits = p.splits;
+            g.st.out = reinterpret_cast<float *>(wpart);
+            g.st.split_stride = (uint64_t)M * N;
+            g.st.ldc = N;
+        }
+        SKL_TRY(launch_gemm(g, ctx->stream));
+    }
+    if (p.splits > 1) {
+        DwReduceArgs d{};
+        d.dtype = g.dtype;
+        d.rows = M;
+        d.n = N;
+        d.splits = p.splits;
+        d.partials = reinterpret_cast<const float *>(wpart);
+        d.plane = p.dma ? (uint64_t)p.Mp * p.Np : (uint64_t)M * N;
+        d.pld = p.dma ? p.Np : N;
+        d.e = oe;
+        SKL_TRY(launch_dw_reduce_opt(d, ctx->stream));
+    }
+    return SKL_OK;
 }
 
 // Common configuration checks of a block descriptor.
@@ -380,17 +524,9 @@ int32_t skl_dense_forward(skl_ctx *ctx, const skl_dense_desc *b, const void *in,
     g.fwd.leaky = b->act == SKL_ACT_LEAKY_RELU ? b->leaky : 0.0f;       // ffn_device.rs:32-35
     g.fwd.p = b->mask_coeff;
     g.fwd.ldc = b->outputs;
-    if (!gemm_direct_ok(g) && use_transposed_operands(b->dtype, batch, b->outputs, b->inputs, in_cols) &&
-        aligned16(in)) {
-        // W^T [N x K] once per call, then the k-contiguous GEMM layout
-        const size_t wt_bytes = (size_t)b->inputs * b->outputs * sizeof(uint16_t);
-        if ((r = ensure_ws(ctx, wt_bytes))) return r;
-        SKL_TRY(launch_transpose_h(b->w, ctx->ws, b->inputs, b->outputs, b->outputs, b->inputs, ctx->stream));
-        g.B = ctx->ws;
-        g.ldb = b->inputs;
-        g.b_kcontig = true;
-    }
-    SKL_TRY(launch_gemm(g, ctx->stream));
+    const GemmPlan plan = plan_gemm(g);
+    if ((r = ensure_ws(ctx, plan.bytes()))) return r;
+    if ((r = exec_gemm(ctx, g, plan, reinterpret_cast<char *>(ctx->ws)))) return r;
 
     if (b->norm != SKL_NORM_DISABLED) {
         RowNormArgs a{};
@@ -465,9 +601,8 @@ int32_t skl_dense_output_error(skl_ctx *ctx, const skl_dense_desc *b, const void
     a.d_prenorm_h = b->dtype == SKL_F16 ? reinterpret_cast<half_t *>(b->d_prenorm_h) : nullptr;
     uint32_t splits = 0;
     if ((r = ensure_cols(ctx, target_rows, b->outputs, &splits))) return r;
-    bool sums = false;
-    SKL_TRY(launch_output_error(a, ctx->cols, splits, &sums, ctx->stream));
-    if (sums) record_cols(ctx, b, target_rows, splits);
+    SKL_TRY(launch_output_error(a, ctx->cols, splits, ctx->stream));
+    record_cols(ctx, b, target_rows, splits);
     return finish(ctx);
 }
 
@@ -490,8 +625,10 @@ static int32_t hidden_error_impl(skl_ctx *ctx, const skl_dense_desc *cur, const 
         if (cur->norm) SKL_CHECK(cur->master_norm_w, SKL_ERR_NULL_POINTER);
     }
     if ((r = zero_dnorm_tail(ctx, cur, batch))) return r;
-    ctx->cs.valid = false;   // cur's d_prenorm is rewritten without column sums
+    ctx->cs.valid = false;
 
+    // s = next.d_prenorm . next.W^T into the workspace (backward.cu:72-77; fp16:
+    // f16(d_prenorm) and the working W, == f16(master) after every update) ...
     GemmLaunch g{};
     g.dtype = cur->dtype;
     g.M = batch;
@@ -501,32 +638,47 @@ static int32_t hidden_error_impl(skl_ctx *ctx, const skl_dense_desc *cur, const 
     g.ldb = next->outputs;
     g.a_kcontig = true;
     g.b_kcontig = true;
-    // fp16: f16(d_prenorm) and the working W (== f16(master) after every update)
     g.A = cur->dtype == SKL_F16 ? next->d_prenorm_h : next->d_prenorm;
     g.B = next->w;
     g.splits = 1;
-    g.op = Op::Hidden;
-    HiddenEpi &h = g.hid;
-    h.predrop = cur->predrop;
-    h.preact = cur->preact;
-    h.mask = cur->mask;
-    h.norm_rstd = cur->norm_rstd;
-    h.centered = cur->centered;
-    h.prenorm = cur->prenorm;
-    h.nw = master_norm_w(cur);
-    h.grad = cur->grad;
-    h.d_prenorm = cur->d_prenorm;
-    h.d_norm_w = cur->d_norm_w;
-    h.d_norm_b = cur->d_norm_b;
-    h.d_prenorm_h = cur->dtype == SKL_F16 ? reinterpret_cast<half_t *>(cur->d_prenorm_h) : nullptr;
-    h.norm = cur->norm;
-    h.act = cur->act;
-    h.leaky = cur->act == SKL_ACT_LEAKY_RELU ? cur->leaky : 0.0f;
-    h.inv_n = 1.0f / (float)cur->outputs;
-    h.inv_m = 1.0f / (float)batch;
-    h.loss_scale = 1.0f;
-    h.ldc = cur->outputs;
-    SKL_TRY(launch_gemm(g, ctx->stream));
+    g.op = Op::InputGrad;
+    const size_t s_bytes = ((size_t)batch * cur->outputs * sizeof(float) + 255) & ~(size_t)255;
+    const GemmPlan plan = plan_gemm(g);
+    if ((r = ensure_ws(ctx, s_bytes + plan.bytes()))) return r;
+    float *sum = reinterpret_cast<float *>(ctx->ws);
+    g.st.out = sum;
+    g.st.ldc = cur->outputs;
+    if ((r = exec_gemm(ctx, g, plan, reinterpret_cast<char *>(ctx->ws) + s_bytes))) return r;
+
+    // ... then act' * mask and the element-local norm gradient (backward.cu:79-100), with
+    // the column sums of d_prenorm / dNorm for cur's backward
+    ErrArgs a{};
+    a.dtype = cur->dtype;
+    a.rows = batch;
+    a.n = cur->outputs;
+    a.norm = cur->norm;
+    a.act = cur->act;
+    a.leaky = cur->act == SKL_ACT_LEAKY_RELU ? cur->leaky : 0.0f;
+    a.inv_n = 1.0f / (float)cur->outputs;
+    a.inv_m = 1.0f / (float)batch;
+    a.loss_scale = 1.0f;
+    a.s = sum;
+    a.predrop = cur->predrop;
+    a.preact = cur->preact;
+    a.mask = cur->mask;
+    a.norm_rstd = cur->norm_rstd;
+    a.centered = cur->centered;
+    a.prenorm = cur->prenorm;
+    a.nw = master_norm_w(cur);
+    a.grad = cur->grad;
+    a.d_prenorm = cur->d_prenorm;
+    a.d_norm_w = cur->d_norm_w;
+    a.d_norm_b = cur->d_norm_b;
+    a.d_prenorm_h = cur->dtype == SKL_F16 ? reinterpret_cast<half_t *>(cur->d_prenorm_h) : nullptr;
+    uint32_t splits = 0;
+    if ((r = ensure_cols(ctx, batch, cur->outputs, &splits))) return r;
+    SKL_TRY(launch_error_from_sum(a, ctx->cols, splits, ctx->stream));
+    record_cols(ctx, cur, batch, splits);
     return SKL_OK;
 }
 
@@ -584,19 +736,8 @@ static int32_t backward_impl(skl_ctx *ctx, const skl_dense_desc *b, const void *
     oe.regularisation = b->regularisation;
     oe.ldc = N;
 
-    const uint32_t tiles = gemm_tiles(b->dtype, K, N);
-    const uint32_t bk = gemm_bk(b->dtype);
-    uint32_t splits = 1;
-    if (tiles < 160 && batch >= 8 * bk) {
-        splits = (256 + tiles - 1) / tiles;
-        const uint32_t max_splits = batch / (4 * bk);
-        if (splits > max_splits) splits = max_splits;
-        if (splits > 16) splits = 16;
-        if (splits < 2) splits = 1;
-    }
-
     // column partial sums for db / dNorm sums: left by the error call just
-    // before, or made here in the workspace
+    // before, or made here in the workspace after the GEMM's region
     const bool cached = cols_match(ctx, b, batch);
     const uint32_t csplits = cached ? ctx->cs.splits : colsum_splits(batch, N);
 
@@ -611,54 +752,16 @@ static int32_t backward_impl(skl_ctx *ctx, const skl_dense_desc *b, const void *
     g.b_kcontig = false;
     g.A = in;
     g.B = f16 ? b->d_prenorm_h : b->d_prenorm;
-    g.splits = splits;
-    g.op = splits == 1 ? Op::DwOpt : Op::DwPartial;
-    g.opt.ldc = N;
-    g.st.ldc = N;
-    const bool transposed = splits == 1 && !gemm_direct_ok(g) &&
-                            use_transposed_operands(b->dtype, K, N, batch, in_cols) && aligned16(in) &&
-                            aligned16(b->d_prenorm_h);
-    const size_t dw_bytes = splits > 1 ? (size_t)splits * K * N * sizeof(float) : 0;
+    g.splits = 1;
+    g.op = Op::DwOpt;
+    g.opt = oe;
+    const GemmPlan plan = plan_gemm(g);
+    const size_t gemm_bytes = (plan.bytes() + 255) & ~(size_t)255;
     const size_t col_bytes = cached ? 0 : (size_t)csplits * 3 * N * sizeof(float);
-    const size_t xt_bytes = transposed ? (size_t)K * batch * sizeof(uint16_t) : 0;
-    const size_t pt_bytes = transposed ? (size_t)N * batch * sizeof(uint16_t) : 0;
-    if ((r = ensure_ws(ctx, dw_bytes + col_bytes + xt_bytes + pt_bytes))) return r;
+    if ((r = ensure_ws(ctx, gemm_bytes + col_bytes))) return r;
     char *ws = reinterpret_cast<char *>(ctx->ws);
-    float *ws_dw = reinterpret_cast<float *>(ws);
-    float *ws_col = reinterpret_cast<float *>(ws + dw_bytes);
-    void *ws_xt = ws + dw_bytes + col_bytes;
-    void *ws_pt = ws + dw_bytes + col_bytes + xt_bytes;
-
-    if (transposed) {
-        // X^T [K x batch] and dP^T [N x batch]: both operands k-contiguous
-        SKL_TRY(launch_transpose_h(in, ws_xt, batch, K, in_cols, batch, ctx->stream));
-        SKL_TRY(launch_transpose_h(b->d_prenorm_h, ws_pt, batch, N, N, batch, ctx->stream));
-        g.A = ws_xt;
-        g.B = ws_pt;
-        g.lda = batch;
-        g.ldb = batch;
-        g.a_kcontig = true;
-        g.b_kcontig = true;
-    }
-    if (splits == 1) {
-        g.op = Op::DwOpt;
-        g.opt = oe;
-        SKL_TRY(launch_gemm(g, ctx->stream));
-    } else {
-        g.op = Op::DwPartial;
-        g.st.out = ws_dw;
-        g.st.split_stride = (uint64_t)K * N;
-        g.st.ldc = N;
-        SKL_TRY(launch_gemm(g, ctx->stream));
-        DwReduceArgs d{};
-        d.dtype = b->dtype;
-        d.rows = K;
-        d.n = N;
-        d.splits = splits;
-        d.partials = ws_dw;
-        d.e = oe;
-        SKL_TRY(launch_dw_reduce_opt(d, ctx->stream));
-    }
+    float *ws_col = reinterpret_cast<float *>(ws + gemm_bytes);
+    if ((r = exec_gemm(ctx, g, plan, ws))) return r;
 
     // -- db, sum dNorm_w, sum dNorm_b and their optimiser steps -----------------------
     VecOptArgs v{};
@@ -751,9 +854,8 @@ int32_t skl_dense_error_from_sum(skl_ctx *ctx, const skl_dense_desc *b, const fl
     a.d_prenorm_h = b->dtype == SKL_F16 ? reinterpret_cast<half_t *>(b->d_prenorm_h) : nullptr;
     uint32_t splits = 0;
     if ((r = ensure_cols(ctx, batch, b->outputs, &splits))) return r;
-    bool sums = false;
-    SKL_TRY(launch_error_from_sum(a, ctx->cols, splits, &sums, ctx->stream));
-    if (sums) record_cols(ctx, b, batch, splits);
+    SKL_TRY(launch_error_from_sum(a, ctx->cols, splits, ctx->stream));
+    record_cols(ctx, b, batch, splits);
     return finish(ctx);
 }
 
@@ -782,7 +884,9 @@ int32_t skl_dense_input_grad(skl_ctx *ctx, const skl_dense_desc *b, uint32_t bat
     g.st.out = dx;
     g.st.split_stride = 0;
     g.st.ldc = b->inputs;
-    SKL_TRY(launch_gemm(g, ctx->stream));
+    const GemmPlan plan = plan_gemm(g);
+    if ((r = ensure_ws(ctx, plan.bytes()))) return r;
+    if ((r = exec_gemm(ctx, g, plan, reinterpret_cast<char *>(ctx->ws)))) return r;
     return finish(ctx);
 }
 

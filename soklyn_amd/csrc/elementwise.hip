@@ -226,91 +226,103 @@ hipError_t launch_softmax(uint32_t dtype, void *out, uint32_t rows, uint32_t n, 
 }
 
 // ---- error kernels ------------------------------------------------------------------
-template <typename T>
-__device__ __forceinline__ void write_err(const ErrArgs &a, uint64_t idx, uint32_t row, uint32_t col, float e) {
-    a.grad[idx] = e;
-    float dp = e;
-    if (a.norm) {
-        const float rstd = to_f32(ldv<T>(a.norm_rstd, a.norm == 3 ? col : row));
-        const float pv = a.norm == 1 ? to_f32(ldv<T>(a.prenorm, idx)) : 0.0f;
-        const float cv = a.norm >= 2 ? to_f32(ldv<T>(a.centered, idx)) : 0.0f;
-        const NormGrad g = norm_grad(a.norm, e, pv, cv, rstd, a.nw[col], a.inv_n, a.inv_m);
-        dp = g.d_prenorm;
-        a.d_norm_w[idx] = g.dnw;
-        a.d_norm_b[idx] = g.dnb;
-    }
-    dp = dp * a.loss_scale;
-    a.d_prenorm[idx] = dp;
-    if (a.d_prenorm_h) a.d_prenorm_h[idx] = (half_t)dp;
-}
-
-// backward.cu:12-56
-template <typename T> __global__ void output_error_kernel(ErrArgs a) {
-    const uint64_t total = (uint64_t)a.rows * a.n;
-    for (uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
-         idx += (uint64_t)gridDim.x * blockDim.x) {
-        const uint32_t row = (uint32_t)(idx / a.n), col = (uint32_t)(idx % a.n);
-        const float o = activation(a.act, to_f32(ldv<T>(a.out, idx)), a.leaky);
-        const float t = to_f32(ldv<T>(a.target, idx));
-        float e = 0.0f;
-        if (a.loss == 0) {
-            e = activation_derivative(a.act, o - t, o, to_f32(ldv<T>(a.preact, idx)), a.leaky);
-        } else if ((a.loss == 1 && a.act == 5) || (a.loss == 2 && a.act == 1)) {
-            e = o - t;
+// A thread owns 4 consecutive elements of one row.  VEC (n % 4 == 0, 16-byte
+// aligned buffers): 16-byte fp32 / 8-byte fp16 accesses; otherwise element
+// accesses of the cnt <= 4 columns that exist.
+template <typename T, bool VEC> struct Grp {
+    __device__ __forceinline__ static f32x4 ld(const void *p, uint64_t i, uint32_t cnt) {
+        if constexpr (VEC) {
+            return load4<T>(p, i);
+        } else {
+            f32x4 v = {0, 0, 0, 0};
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j)
+                if (j < cnt) v[j] = to_f32(ldv<T>(p, i + j));
+            return v;
         }
-        write_err<T>(a, idx, row, col, e);
     }
-}
-
-// backward.cu:79-100 with s supplied
-template <typename T> __global__ void error_from_sum_kernel(ErrArgs a) {
-    const uint64_t total = (uint64_t)a.rows * a.n;
-    for (uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
-         idx += (uint64_t)gridDim.x * blockDim.x) {
-        const uint32_t row = (uint32_t)(idx / a.n), col = (uint32_t)(idx % a.n);
-        const float d = activation_derivative(a.act, a.s[idx], to_f32(ldv<T>(a.predrop, idx)),
-                                              to_f32(ldv<T>(a.preact, idx)), a.leaky);
-        write_err<T>(a, idx, row, col, to_f32(ldv<T>(a.mask, idx)) * d);
+    __device__ __forceinline__ static f32x4 ldf(const float *p, uint64_t i, uint32_t cnt, bool nt = false) {
+        if constexpr (VEC) {
+            return nt ? __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p + i))
+                      : *reinterpret_cast<const f32x4 *>(p + i);
+        } else {
+            f32x4 v = {0, 0, 0, 0};
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j)
+                if (j < cnt) v[j] = p[i + j];
+            return v;
+        }
     }
-}
+    __device__ __forceinline__ static void stf(float *p, uint64_t i, f32x4 v, uint32_t cnt, bool nt = false) {
+        if constexpr (VEC) {
+            if (nt)
+                __builtin_nontemporal_store(v, reinterpret_cast<f32x4 *>(p + i));
+            else
+                *reinterpret_cast<f32x4 *>(p + i) = v;
+        } else {
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j)
+                if (j < cnt) p[i + j] = v[j];
+        }
+    }
+    __device__ __forceinline__ static void sth(half_t *p, uint64_t i, f32x4 v, uint32_t cnt) {
+        if constexpr (VEC) {
+            store4<half_t>(p, i, v);
+        } else {
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j)
+                if (j < cnt) p[i + j] = (half_t)v[j];
+        }
+    }
+};
 
-// Vector forms: each thread owns 4 consecutive elements of one row (n % 4 == 0,
-// 16-byte aligned buffers): 16-byte fp32 / 8-byte fp16 accesses, 32-bit indexing.
 // The three values of one 4-column group that feed the column sums of backward.cu:187-194.
 struct ErrSums4 {
     f32x4 dp, dnw, dnb;
 };
 
-template <typename T>
-__device__ __forceinline__ ErrSums4 write_err4(const ErrArgs &a, uint64_t idx, uint32_t row, uint32_t col, f32x4 e) {
-    __builtin_nontemporal_store(e, reinterpret_cast<f32x4 *>(a.grad + idx));
+// grad = e; the element-local norm gradient (util.cu:175-215) into d_prenorm and
+// dNorm; d_prenorm scaled by the loss scale; its fp16 copy for the GEMMs.
+template <typename T, bool VEC>
+__device__ __forceinline__ ErrSums4 write_err4(const ErrArgs &a, uint64_t idx, uint32_t row, uint32_t col,
+                                               uint32_t cnt, f32x4 e) {
+    typedef Grp<T, VEC> G;
+    G::stf(a.grad, idx, e, cnt, true);
     ErrSums4 o;
     o.dp = e;
     o.dnw = o.dnb = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     if (a.norm) {
-        const f32x4 pv = a.norm == 1 ? load4<T>(a.prenorm, idx) : f32x4{0, 0, 0, 0};
-        const f32x4 cv = a.norm >= 2 ? load4<T>(a.centered, idx) : f32x4{0, 0, 0, 0};
-        const f32x4 nw = *reinterpret_cast<const f32x4 *>(a.nw + col);
+        const f32x4 pv = a.norm == 1 ? G::ld(a.prenorm, idx, cnt) : f32x4{0, 0, 0, 0};
+        const f32x4 cv = a.norm >= 2 ? G::ld(a.centered, idx, cnt) : f32x4{0, 0, 0, 0};
+        const f32x4 nw = G::ldf(a.nw, col, cnt);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const float rstd = to_f32(ldv<T>(a.norm_rstd, a.norm == 3 ? col + j : row));
+            const float rstd = to_f32(ldv<T>(a.norm_rstd, a.norm == 3 ? col + (j < (int)cnt ? j : 0) : row));
             const NormGrad g = norm_grad(a.norm, e[j], pv[j], cv[j], rstd, nw[j], a.inv_n, a.inv_m);
             o.dp[j] = g.d_prenorm;
             o.dnw[j] = g.dnw;
             o.dnb[j] = g.dnb;
         }
-        *reinterpret_cast<f32x4 *>(a.d_norm_w + idx) = o.dnw;
-        *reinterpret_cast<f32x4 *>(a.d_norm_b + idx) = o.dnb;
+        G::stf(a.d_norm_w, idx, o.dnw, cnt);
+        G::stf(a.d_norm_b, idx, o.dnb, cnt);
     }
     o.dp = o.dp * a.loss_scale;
-    __builtin_nontemporal_store(o.dp, reinterpret_cast<f32x4 *>(a.d_prenorm + idx));
-    if (a.d_prenorm_h) store4<half_t>(a.d_prenorm_h, idx, o.dp);
+    G::stf(a.d_prenorm, idx, o.dp, cnt, true);
+    if (a.d_prenorm_h) G::sth(a.d_prenorm_h, idx, o.dp, cnt);
+    if (!VEC) {
+        // columns past n add nothing to the sums
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j)
+            if (j >= cnt) o.dp[j] = o.dnw[j] = o.dnb[j] = 0.0f;
+    }
     return o;
 }
 
 // Loss delta of one 4-column group (backward.cu:24-45).
-template <typename T> __device__ __forceinline__ f32x4 output_err4(const ErrArgs &a, uint64_t idx) {
-    const f32x4 out = load4<T>(a.out, idx), tg = load4<T>(a.target, idx), pre = load4<T>(a.preact, idx);
+template <typename T, bool VEC>
+__device__ __forceinline__ f32x4 output_err4(const ErrArgs &a, uint64_t idx, uint32_t cnt) {
+    typedef Grp<T, VEC> G;
+    const f32x4 out = G::ld(a.out, idx, cnt), tg = G::ld(a.target, idx, cnt), pre = G::ld(a.preact, idx, cnt);
     f32x4 e;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -326,100 +338,85 @@ template <typename T> __device__ __forceinline__ f32x4 output_err4(const ErrArgs
     return e;
 }
 
-// Error + column sums in one pass.  Workgroup (x, y) owns the columns
-// [1024 UC x, 1024 UC (x + 1)) of the rows [y per, (y + 1) per): a thread owns
-// UC 4-column groups 1024 apart, loads UR rows of all of them before computing
-// any (UR x UC x 40 bytes in flight), writes grad / d_prenorm (/ dNorm) and
-// adds d_prenorm, dNorm_w and dNorm_b into running column sums, rows in
-// ascending order.  The sums go to partials[y][k][n] (k = 0 d_prenorm,
-// 1 dNorm_w, 2 dNorm_b; 1 and 2 only with a norm), the inputs of the bias /
-// norm-parameter update, so the backward does not read the three [rows x n]
-// buffers again.
-template <typename T, bool FROM_SUM, int UR, int UC>
+// Error + column sums in one pass (backward.cu:12-56 for the output layer,
+// 79-100 for a supplied sum s).  Workgroup (x, y) owns the columns
+// [1024 x, 1024 (x + 1)) of the rows [y per, (y + 1) per): a thread owns one
+// 4-column group, loads ERR_UR rows of its operands before computing any
+// (ERR_UR x 40 bytes in flight), writes grad / d_prenorm (/ dNorm) and adds
+// d_prenorm, dNorm_w and dNorm_b into running column sums, rows in ascending
+// order.  The sums go to partials[y][k][n] (k = 0 d_prenorm, 1 dNorm_w,
+// 2 dNorm_b; 1 and 2 only with a norm), the inputs of the bias / norm-
+// parameter update, so the backward does not read the three [rows x n]
+// buffers again.  4 rows per thread and ~1024 workgroups: of the shapes
+// measured on the C3 step (rows x column groups per thread in {4x1, 2x2, 1x4,
+// 2x4}, 512 to 2048 workgroups) the fastest, both alone and between the GEMMs.
+constexpr int ERR_UR = 4;
+template <typename T, bool FROM_SUM, bool VEC>
 __global__ void __launch_bounds__(256) error_cols_kernel(ErrArgs a, float *__restrict__ partials, uint32_t per) {
-    const uint32_t cbase = blockIdx.x * (1024 * UC) + threadIdx.x * 4;
-    if (cbase >= a.n) return;
+    typedef Grp<T, VEC> G;
+    const uint32_t c = blockIdx.x * 1024 + threadIdx.x * 4;
+    if (c >= a.n) return;
+    const uint32_t cnt = min(4u, a.n - c);
     const uint32_t r0 = blockIdx.y * per;
     const uint32_t r1 = min(a.rows, r0 + per);
-    f32x4 sdp[UC], snw[UC], snb[UC];
-#pragma unroll
-    for (int v = 0; v < UC; ++v) sdp[v] = snw[v] = snb[v] = f32x4{0, 0, 0, 0};
-    for (uint32_t rb = r0; rb < r1; rb += UR) {
-        f32x4 x0[UR][UC], x1[UR][UC], x2[UR][UC], x3[UR][UC];
+    f32x4 sdp = {0, 0, 0, 0}, snw = {0, 0, 0, 0}, snb = {0, 0, 0, 0};
+    for (uint32_t rb = r0; rb < r1; rb += ERR_UR) {
+        f32x4 x0[ERR_UR], x1[ERR_UR], x2[ERR_UR], x3[ERR_UR];
         if constexpr (FROM_SUM) {
 #pragma unroll
-            for (int u = 0; u < UR; ++u) {
+            for (int u = 0; u < ERR_UR; ++u) {
                 if (rb + u >= r1) break;
-#pragma unroll
-                for (int v = 0; v < UC; ++v) {
-                    const uint32_t c = cbase + 1024 * v;
-                    if (c >= a.n) break;
-                    const uint32_t idx = (rb + u) * a.n + c;
-                    x0[u][v] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(a.s + idx));
-                    x1[u][v] = load4<T>(a.predrop, idx);
-                    x2[u][v] = load4<T>(a.preact, idx);
-                    x3[u][v] = load4<T>(a.mask, idx);
-                }
+                const uint64_t idx = (uint64_t)(rb + u) * a.n + c;
+                x0[u] = G::ldf(a.s, idx, cnt, true);
+                x1[u] = G::ld(a.predrop, idx, cnt);
+                x2[u] = G::ld(a.preact, idx, cnt);
+                x3[u] = G::ld(a.mask, idx, cnt);
             }
         }
 #pragma unroll
-        for (int u = 0; u < UR; ++u) {
+        for (int u = 0; u < ERR_UR; ++u) {
             const uint32_t row = rb + u;
             if (row >= r1) break;
+            const uint64_t idx = (uint64_t)row * a.n + c;
+            f32x4 e;
+            if constexpr (FROM_SUM) {
 #pragma unroll
-            for (int v = 0; v < UC; ++v) {
-                const uint32_t c = cbase + 1024 * v;
-                if (c >= a.n) break;
-                const uint32_t idx = row * a.n + c;
-                f32x4 e;
-                if constexpr (FROM_SUM) {
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        e[j] = x3[u][v][j] * activation_derivative(a.act, x0[u][v][j], x1[u][v][j], x2[u][v][j], a.leaky);
-                } else {
-                    e = output_err4<T>(a, idx);
-                }
-                const ErrSums4 o = write_err4<T>(a, idx, row, c, e);
-                sdp[v] += o.dp;
-                snw[v] += o.dnw;
-                snb[v] += o.dnb;
+                for (int j = 0; j < 4; ++j)
+                    e[j] = x3[u][j] * activation_derivative(a.act, x0[u][j], x1[u][j], x2[u][j], a.leaky);
+            } else {
+                e = output_err4<T, VEC>(a, idx, cnt);
             }
+            const ErrSums4 o = write_err4<T, VEC>(a, idx, row, c, cnt, e);
+            sdp += o.dp;
+            snw += o.dnw;
+            snb += o.dnb;
         }
     }
-#pragma unroll
-    for (int v = 0; v < UC; ++v) {
-        const uint32_t c = cbase + 1024 * v;
-        if (c >= a.n) break;
-        float *p = partials + (uint64_t)blockIdx.y * 3 * a.n + c;
-        *reinterpret_cast<f32x4 *>(p) = sdp[v];
-        if (a.norm) {
-            *reinterpret_cast<f32x4 *>(p + a.n) = snw[v];
-            *reinterpret_cast<f32x4 *>(p + 2 * a.n) = snb[v];
-        }
+    float *p = partials + (uint64_t)blockIdx.y * 3 * a.n + c;
+    G::stf(p, 0, sdp, cnt);
+    if (a.norm) {
+        G::stf(p + a.n, 0, snw, cnt);
+        G::stf(p + 2 * a.n, 0, snb, cnt);
     }
 }
 
 static bool a16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-static bool err_vec_ok(const ErrArgs &a, bool from_sum) {
-    if ((a.n & 3u) != 0 || (uint64_t)a.rows * a.n >= (1ull << 32)) return false;
+static bool err_vec_ok(const ErrArgs &a, bool from_sum, const float *partials) {
+    if ((a.n & 3u) != 0) return false;
     const void *ptrs[] = {a.grad, a.d_prenorm, a.d_prenorm_h, a.preact, a.norm ? a.nw : nullptr,
                           a.norm ? a.d_norm_w : nullptr, a.norm ? a.d_norm_b : nullptr,
                           a.norm == 1 ? a.prenorm : nullptr, a.norm >= 2 ? a.centered : nullptr,
-                          from_sum ? a.s : a.out, from_sum ? a.predrop : a.target, from_sum ? a.mask : nullptr};
+                          from_sum ? a.s : a.out, from_sum ? a.predrop : a.target, from_sum ? a.mask : nullptr,
+                          partials};
     for (const void *p : ptrs)
         if (p && !a16(p)) return false;
     return true;
 }
 
-// 4 rows x 1 column group per thread and ~1024 workgroups: of the shapes
-// measured on the C3 step (UR x UC in {4x1, 2x2, 1x4, 2x4}, 512 to 2048
-// workgroups) the fastest, both alone and between the GEMMs of the step.
-constexpr int ERR_UR = 4, ERR_UC = 1;
-
-// Row splits of the fused error + column-sum kernels: ~1024 workgroups.
+// Row splits of the error kernels: ~1024 workgroups.
 uint32_t err_col_splits(uint32_t rows, uint32_t n) {
-    const uint32_t col_blocks = cdiv(n, 1024 * ERR_UC);
+    const uint32_t col_blocks = cdiv(n, 1024);
     uint32_t sp = cdiv(1024, col_blocks);
     const uint32_t cap = cdiv(rows, 16);
     if (sp > cap) sp = cap;
@@ -427,41 +424,32 @@ uint32_t err_col_splits(uint32_t rows, uint32_t n) {
     return sp < 1 ? 1 : sp;
 }
 
-template <bool FROM_SUM>
-static hipError_t launch_error(const ErrArgs &a, float *partials, uint32_t splits, hipStream_t s) {
-    const uint64_t total = (uint64_t)a.rows * a.n;
-    if (total == 0) return hipSuccess;
-    if (partials) {
-        const uint32_t per = cdiv(a.rows, splits);
-        const dim3 g(cdiv(a.n, 1024 * ERR_UC), splits);
-        if (a.dtype == 1)
-            hipLaunchKernelGGL((error_cols_kernel<half_t, FROM_SUM, ERR_UR, ERR_UC>), g, dim3(256), 0, s, a,
-                               partials, per);
-        else
-            hipLaunchKernelGGL((error_cols_kernel<float, FROM_SUM, ERR_UR, ERR_UC>), g, dim3(256), 0, s, a,
-                               partials, per);
-    } else if (FROM_SUM) {
-        if (a.dtype == 1)
-            hipLaunchKernelGGL(error_from_sum_kernel<half_t>, grid_for(total, 256), dim3(256), 0, s, a);
-        else
-            hipLaunchKernelGGL(error_from_sum_kernel<float>, grid_for(total, 256), dim3(256), 0, s, a);
-    } else {
-        if (a.dtype == 1)
-            hipLaunchKernelGGL(output_error_kernel<half_t>, grid_for(total, 256), dim3(256), 0, s, a);
-        else
-            hipLaunchKernelGGL(output_error_kernel<float>, grid_for(total, 256), dim3(256), 0, s, a);
-    }
+template <bool FROM_SUM, typename T>
+static void launch_error_t(const ErrArgs &a, float *partials, uint32_t splits, hipStream_t s) {
+    const uint32_t per = cdiv(a.rows, splits);
+    const dim3 g(cdiv(a.n, 1024), splits);
+    if (err_vec_ok(a, FROM_SUM, partials))
+        hipLaunchKernelGGL((error_cols_kernel<T, FROM_SUM, true>), g, dim3(256), 0, s, a, partials, per);
+    else
+        hipLaunchKernelGGL((error_cols_kernel<T, FROM_SUM, false>), g, dim3(256), 0, s, a, partials, per);
+}
+
+hipError_t launch_output_error(const ErrArgs &a, float *partials, uint32_t splits, hipStream_t s) {
+    if ((uint64_t)a.rows * a.n == 0) return hipSuccess;
+    if (a.dtype == 1)
+        launch_error_t<false, half_t>(a, partials, splits, s);
+    else
+        launch_error_t<false, float>(a, partials, splits, s);
     return hipGetLastError();
 }
 
-hipError_t launch_output_error(const ErrArgs &a, float *partials, uint32_t splits, bool *sums, hipStream_t s) {
-    *sums = partials && err_vec_ok(a, false);
-    return launch_error<false>(a, *sums ? partials : nullptr, splits, s);
-}
-
-hipError_t launch_error_from_sum(const ErrArgs &a, float *partials, uint32_t splits, bool *sums, hipStream_t s) {
-    *sums = partials && err_vec_ok(a, true);
-    return launch_error<true>(a, *sums ? partials : nullptr, splits, s);
+hipError_t launch_error_from_sum(const ErrArgs &a, float *partials, uint32_t splits, hipStream_t s) {
+    if ((uint64_t)a.rows * a.n == 0) return hipSuccess;
+    if (a.dtype == 1)
+        launch_error_t<true, half_t>(a, partials, splits, s);
+    else
+        launch_error_t<true, float>(a, partials, splits, s);
+    return hipGetLastError();
 }
 
 // ---- column sums (backward.cu:187-194) + vector optimiser (backward.cu:198-225) -------
@@ -584,8 +572,10 @@ template <typename T> __global__ void dw_reduce_opt_kernel(DwReduceArgs a) {
     const uint64_t total = (uint64_t)a.rows * a.n;
     for (uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
          idx += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t r = idx / a.n, c = idx - r * a.n;
+        const float *pp = a.partials + r * a.pld + c;
         float s = 0.0f;
-        for (uint32_t sp = 0; sp < a.splits; ++sp) s += a.partials[(uint64_t)sp * total + idx];
+        for (uint32_t sp = 0; sp < a.splits; ++sp) s += pp[(uint64_t)sp * a.plane];
         const OptEpi &e = a.e;
         float p = e.master[idx], v = e.dv[idx], mm = e.dm[idx];
         optimiser_step(p, v, mm, s * kLossScaleInv, e.inv_m, e.lr, e.clamp, e.opt, e.regularisation, e.regu_coeff,
@@ -607,44 +597,41 @@ hipError_t launch_dw_reduce_opt(const DwReduceArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
-// ---- fp16 transpose (64 x 64 LDS tiles) ---------------------------------------------------
-// out[c][r] = in[r][c]; in is [rows x cols] (leading dim ld_in), out is [cols x rows]
-// (leading dim ld_out).  Loads are 16-byte row chunks; stores are 16-byte column
-// chunks gathered from LDS.  rows, cols, ld_in, ld_out are multiples of 8.
-__global__ void __launch_bounds__(256) transpose_h_kernel(const half_t *__restrict__ in, half_t *__restrict__ out,
-                                                          uint32_t rows, uint32_t cols, uint32_t ld_in,
-                                                          uint32_t ld_out) {
-    __shared__ half_t tile[64][64 + 8];
-    const uint32_t r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
-    const uint32_t t = threadIdx.x;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const uint32_t q = t + i * 256;              // 512 chunks of 8 halves
-        const uint32_t r = q >> 3, c = (q & 7u) * 8;
+// ---- zero-padded fp16 copy (operand staging for the 256x256 GEMM) -----------------------
+// out[r][c] = (r < rows && c < cols) ? in[r ld + c] : 0 for r < rows_p, c < cols_p
+// (cols_p a multiple of 8): a thread writes 8 consecutive halves (16 bytes).
+__global__ void __launch_bounds__(256) pad_h_kernel(const half_t *__restrict__ in, uint32_t rows, uint32_t cols,
+                                                    uint32_t ld, half_t *__restrict__ out, uint32_t rows_p,
+                                                    uint32_t cols_p, uint32_t vec_in) {
+    const uint32_t gpr = cols_p / 8;
+    const uint64_t total = (uint64_t)rows_p * gpr;
+    for (uint64_t q = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; q < total;
+         q += (uint64_t)gridDim.x * blockDim.x) {
+        const uint32_t r = (uint32_t)(q / gpr), c = (uint32_t)(q % gpr) * 8;
         u32x4_t v = {0, 0, 0, 0};
-        if (r0 + r < rows && c0 + c < cols)
-            v = *reinterpret_cast<const u32x4_t *>(in + (uint64_t)(r0 + r) * ld_in + c0 + c);
-        *reinterpret_cast<u32x4_t *>(&tile[r][c]) = v;
-    }
-    __syncthreads();
+        if (r < rows && c < cols) {
+            const half_t *src = in + (uint64_t)r * ld + c;
+            if (vec_in && c + 8 <= cols) {
+                v = *reinterpret_cast<const u32x4_t *>(src);
+            } else {
+                half_t h[8];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const uint32_t q = t + i * 256;
-        const uint32_t oc = q >> 3, orr = (q & 7u) * 8;   // out row = in col, out col = in row
-        if (c0 + oc >= cols || r0 + orr >= rows) continue;
-        half_t h[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) h[e] = tile[orr + e][oc];
-        *reinterpret_cast<u32x4_t *>(out + (uint64_t)(c0 + oc) * ld_out + r0 + orr) = __builtin_bit_cast(u32x4_t, h);
+                for (uint32_t e = 0; e < 8; ++e) h[e] = c + e < cols ? src[e] : (half_t)0;
+                v = __builtin_bit_cast(u32x4_t, h);
+            }
+        }
+        *reinterpret_cast<u32x4_t *>(out + (uint64_t)r * cols_p + c) = v;
     }
 }
 
-hipError_t launch_transpose_h(const void *in, void *out, uint32_t rows, uint32_t cols, uint32_t ld_in,
-                              uint32_t ld_out, hipStream_t s) {
-    if (rows == 0 || cols == 0) return hipSuccess;
-    hipLaunchKernelGGL(transpose_h_kernel, dim3(cdiv(cols, 64), cdiv(rows, 64)), dim3(256), 0, s,
-                       reinterpret_cast<const half_t *>(in), reinterpret_cast<half_t *>(out), rows, cols, ld_in,
-                       ld_out);
+hipError_t launch_pad_h(const void *in, uint32_t rows, uint32_t cols, uint32_t ld, void *out, uint32_t rows_p,
+                        uint32_t cols_p, hipStream_t s) {
+    if (cols_p % 8 || rows_p < rows || cols_p < cols || !a16(out)) return hipErrorInvalidValue;
+    const uint64_t groups = (uint64_t)rows_p * (cols_p / 8);
+    if (groups == 0) return hipSuccess;
+    const uint32_t vec_in = (ld % 8 == 0 && a16(in)) ? 1u : 0u;
+    hipLaunchKernelGGL(pad_h_kernel, grid_for(groups, 256), dim3(256), 0, s, reinterpret_cast<const half_t *>(in),
+                       rows, cols, ld, reinterpret_cast<half_t *>(out), rows_p, cols_p, vec_in);
     return hipGetLastError();
 }
 

@@ -49,8 +49,9 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 struct GemmShape {
     uint32_t M, N, K;        // output rows, output cols, reduction length
     uint32_t lda, ldb;       // leading dimensions (elements)
-    uint32_t k_per_split;    // reduction length per blockIdx.z (multiple of BK)
+    uint32_t k_per_split;    // reduction length per split (multiple of BK)
     uint32_t tiles_m, tiles_n;
+    uint32_t mv, nv;         // 256x256 kernel on zero-padded operands: the real output extent
 };
 
 // Workgroup barrier that orders LDS only: wait for this wave's LDS accesses,

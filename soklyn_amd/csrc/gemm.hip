@@ -26,6 +26,7 @@ template <typename T> __device__ __forceinline__ void st_t(void *p, uint64_t i, 
 template <typename T> struct EpiFwdK {
     typedef FwdEpi Params;
     __device__ __forceinline__ static uint32_t ldc(const FwdEpi &e) { return e.ldc; }
+    __device__ __forceinline__ static FwdEpi at_split(const FwdEpi &e, uint32_t) { return e; }
     struct Col { f32x4 bias; };
     struct Pre {};
     __device__ __forceinline__ static Col column(const FwdEpi &e, uint32_t n) {
@@ -97,93 +98,16 @@ template <typename T> struct EpiFwdK {
     }
 };
 
-// ---- hidden error: act' * mask, element-local norm gradient --------------------
-template <typename T> struct EpiHiddenK {
-    typedef HiddenEpi Params;
-    __device__ __forceinline__ static uint32_t ldc(const HiddenEpi &e) { return e.ldc; }
-    // norm 1 (RMS) reads prenorm, 2 (LN) / 3 (BN) read centered; rstd is per row
-    // for RMS / LN and per column for BN.
-    struct Col { f32x4 nw, rstd; };
-    struct Pre { f32x4 pd, pa, mk, aux; float rstd; };
-    __device__ __forceinline__ static Col column(const HiddenEpi &e, uint32_t n) {
-        Col c;
-        c.nw = e.norm ? *reinterpret_cast<const f32x4 *>(e.nw + n) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        c.rstd = e.norm == 3 ? load4<T>(e.norm_rstd, n) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        return c;
-    }
-    __device__ __forceinline__ static void load(const HiddenEpi &e, uint64_t idx, uint32_t m, Pre &p) {
-        p.pd = load4<T>(e.predrop, idx);
-        p.pa = load4<T>(e.preact, idx);
-        p.mk = load4<T>(e.mask, idx);
-        if (e.norm) p.aux = load4<T>(e.norm == 1 ? e.prenorm : e.centered, idx);
-        if (e.norm == 1 || e.norm == 2) p.rstd = to_f32(ld_t<T>(e.norm_rstd, m));
-    }
-    __device__ __forceinline__ static void finish(const HiddenEpi &e, uint64_t idx, uint32_t, uint32_t, floatx4 v,
-                                                  const Col &col, const Pre &p) {
-        f32x4 err;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) err[j] = p.mk[j] * activation_derivative(e.act, v[j], p.pd[j], p.pa[j], e.leaky);
-        *reinterpret_cast<f32x4 *>(e.grad + idx) = err;
-        f32x4 dp = err;
-        if (e.norm) {
-            f32x4 dnw, dnb;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float rstd = e.norm == 3 ? col.rstd[j] : p.rstd;
-                const float pv = e.norm == 1 ? p.aux[j] : 0.0f;
-                const float cv = e.norm >= 2 ? p.aux[j] : 0.0f;
-                const NormGrad g = norm_grad(e.norm, err[j], pv, cv, rstd, col.nw[j], e.inv_n, e.inv_m);
-                dp[j] = g.d_prenorm;
-                dnw[j] = g.dnw;
-                dnb[j] = g.dnb;
-            }
-            *reinterpret_cast<f32x4 *>(e.d_norm_w + idx) = dnw;
-            *reinterpret_cast<f32x4 *>(e.d_norm_b + idx) = dnb;
-        }
-        dp = dp * e.loss_scale;
-        *reinterpret_cast<f32x4 *>(e.d_prenorm + idx) = dp;
-        if (e.d_prenorm_h) store4<half_t>(e.d_prenorm_h, idx, dp);
-    }
-    __device__ __forceinline__ static void apply(const HiddenEpi &e, const GemmShape &sh, uint32_t m,
-                                                 uint32_t n, floatx4 v, uint32_t) {
-        if (m >= sh.M) return;
-        if (n + 3 < sh.N && (e.ldc & 3u) == 0) {
-            const uint64_t idx = (uint64_t)m * e.ldc + n;
-            Pre p;
-            load(e, idx, m, p);
-            finish(e, idx, m, n, v, column(e, n), p);
-            return;
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t c = n + j;
-            if (c >= sh.N) break;
-            const uint64_t idx = (uint64_t)m * e.ldc + c;
-            const float d = activation_derivative(e.act, v[j], to_f32(ld_t<T>(e.predrop, idx)),
-                                                  to_f32(ld_t<T>(e.preact, idx)), e.leaky);
-            const float err = to_f32(ld_t<T>(e.mask, idx)) * d;
-            e.grad[idx] = err;
-            float dp = err;
-            if (e.norm) {
-                const float rstd = to_f32(ld_t<T>(e.norm_rstd, e.norm == 3 ? c : m));
-                const float pv = e.norm == 1 ? to_f32(ld_t<T>(e.prenorm, idx)) : 0.0f;
-                const float cv = e.norm >= 2 ? to_f32(ld_t<T>(e.centered, idx)) : 0.0f;
-                const NormGrad g = norm_grad(e.norm, err, pv, cv, rstd, e.nw[c], e.inv_n, e.inv_m);
-                dp = g.d_prenorm;
-                e.d_norm_w[idx] = g.dnw;
-                e.d_norm_b[idx] = g.dnb;
-            }
-            dp = dp * e.loss_scale;
-            e.d_prenorm[idx] = dp;
-            if (e.d_prenorm_h) e.d_prenorm_h[idx] = (half_t)dp;
-        }
-    }
-};
-
 // ---- plain fp32 store (input gradient; split-K partials) -----------------------
 struct EpiStoreK {
     typedef StoreEpi Params;
     __device__ __forceinline__ static uint32_t ldc(const StoreEpi &e) { return e.ldc; }
+    // the partial plane of split-K slice `split`
+    __device__ __forceinline__ static StoreEpi at_split(const StoreEpi &e, uint32_t split) {
+        StoreEpi r = e;
+        r.out += (uint64_t)split * e.split_stride;
+        return r;
+    }
     struct Col {};
     struct Pre {};
     __device__ __forceinline__ static Col column(const StoreEpi &, uint32_t) { return Col{}; }
@@ -210,6 +134,7 @@ struct EpiStoreK {
 template <typename T> struct EpiOptK {
     typedef OptEpi Params;
     __device__ __forceinline__ static uint32_t ldc(const OptEpi &e) { return e.ldc; }
+    __device__ __forceinline__ static OptEpi at_split(const OptEpi &e, uint32_t) { return e; }
     struct Col {};
     struct Pre { floatx4 p, dv, dm; };
     __device__ __forceinline__ static Col column(const OptEpi &, uint32_t) { return Col{}; }
@@ -328,7 +253,6 @@ template <class C> static hipError_t dispatch_op(const GemmLaunch &g, hipStream_
     case Op::Fwd:
         return g.b_kcontig ? dispatch_vec<C, true, true, EpiFwdK<T>>(g, g.fwd, s)
                            : dispatch_vec<C, true, false, EpiFwdK<T>>(g, g.fwd, s);
-    case Op::Hidden: return dispatch_vec<C, true, true, EpiHiddenK<T>>(g, g.hid, s);
     case Op::InputGrad: return dispatch_vec<C, true, true, EpiStoreK>(g, g.st, s);
     // dW also runs on transposed copies of X and dP (both k-contiguous)
     case Op::DwPartial:
@@ -347,7 +271,6 @@ template <class C> static hipError_t dispatch_kk(const GemmLaunch &g, hipStream_
     typedef typename C::type T;
     switch (g.op) {
     case Op::Fwd: return dispatch_vec<C, true, true, EpiFwdK<T>>(g, g.fwd, s);
-    case Op::Hidden: return dispatch_vec<C, true, true, EpiHiddenK<T>>(g, g.hid, s);
     case Op::InputGrad:
     case Op::DwPartial: return dispatch_vec<C, true, true, EpiStoreK>(g, g.st, s);
     case Op::DwOpt: return dispatch_vec<C, true, true, EpiOptK<T>>(g, g.opt, s);
@@ -369,10 +292,9 @@ uint32_t gemm_tiles(uint32_t dtype, uint32_t M, uint32_t N) {
 
 uint32_t gemm_bk(uint32_t dtype) { return dtype == 1 ? 64 : 32; }
 
-// The direct-to-LDS 4-wave kernel: fp16, whole 256x256 tiles, K a multiple of
-// 128 (two k-tiles), 32-bit operand offsets.
-// SOKLYN_GEMM_DMA=0 selects the register-staged kernel instead (A/B comparisons).
-static bool dma_enabled() {
+// The direct-to-LDS 256x256 kernel (gemm_dma.h).  SOKLYN_GEMM_DMA=0 selects
+// the register-staged kernels instead (A/B comparisons).
+bool gemm_dma_enabled() {
     static bool on = [] {
         const char *e = getenv("SOKLYN_GEMM_DMA");
         return !(e && atoi(e) == 0);
@@ -390,32 +312,43 @@ static bool dma_layout_ok(const GemmLaunch &g) {
     return false;
 }
 
-static bool dma_ok(const GemmLaunch &g) {
-    if (!dma_enabled() || g.dtype != 1 || !dma_layout_ok(g)) return false;
-    if ((g.M % 256) || (g.N % 256) || (g.K % 128) || g.K == 0 || (g.splits && g.splits != 1)) return false;
-    if (!vec_ok(g, 8)) return false;
-    // the batched epilogue accesses 4 columns at a time without edge checks
-    uint32_t ldc = 0;
+static uint32_t epi_ldc(const GemmLaunch &g) {
     switch (g.op) {
-    case Op::Fwd: ldc = g.fwd.ldc; break;
-    case Op::Hidden: ldc = g.hid.ldc; break;
+    case Op::Fwd: return g.fwd.ldc;
     case Op::InputGrad:
-    case Op::DwPartial: ldc = g.st.ldc; break;
-    case Op::DwOpt: ldc = g.opt.ldc; break;
+    case Op::DwPartial: return g.st.ldc;
+    case Op::DwOpt: return g.opt.ldc;
     }
-    if (ldc % 4) return false;
-    // 32-bit byte offsets within each operand
+    return 0;
+}
+
+// The operands as given fit the 256x256 kernel: fp16, whole tiles, K a multiple
+// of 128 (two k-tiles), 16-byte rows, 32-bit byte offsets within each operand.
+bool gemm_dma_shape_ok(const GemmLaunch &g) {
+    if (!gemm_dma_enabled() || g.dtype != 1 || !dma_layout_ok(g)) return false;
+    if ((g.M % 256) || (g.N % 256) || (g.K % 128) || g.K == 0) return false;
+    if (!vec_ok(g, 8)) return false;
     const uint64_t a_rows = g.a_kcontig ? g.M : g.K, b_rows = g.b_kcontig ? g.N : g.K;
     return a_rows * g.lda * 2 < (1ull << 32) && b_rows * g.ldb * 2 < (1ull << 32);
 }
 
-bool gemm_direct_ok(const GemmLaunch &g) { return gemm_large_tile(g.dtype, g.M, g.N) && dma_ok(g); }
+// Whole output tiles with a 4-aligned leading dimension: the batched epilogue.
+static bool dma_full_epilogue(const GemmLaunch &g) {
+    const uint32_t mv = g.mv ? g.mv : g.M, nv = g.nv ? g.nv : g.N;
+    return mv == g.M && nv == g.N && epi_ldc(g) % 4 == 0;
+}
+
+bool gemm_direct_ok(const GemmLaunch &g) {
+    return gemm_large_tile(g.dtype, g.M, g.N) && gemm_dma_shape_ok(g) && dma_full_epilogue(g) &&
+           (g.splits == 0 || g.splits == 1);
+}
 
 // Waves per workgroup: 8 when an operand is read through the transposing LDS
 // path (its 8-byte reads leave one wave per SIMD waiting on LDS latency), 4
 // when both operands are k-contiguous (see gemm_dma.h).
 template <class Epi, bool AK, bool BK_>
-static hipError_t run_dma(const GemmLaunch &g, const typename Epi::Params &p, hipStream_t s) {
+static hipError_t run_dma(const GemmLaunch &g, const typename Epi::Params &p, uint32_t splits, uint32_t kps,
+                          hipStream_t s) {
     constexpr int NW = (AK && BK_) ? 4 : 8;
     GemmShape sh{};
     sh.M = g.M;
@@ -423,37 +356,56 @@ static hipError_t run_dma(const GemmLaunch &g, const typename Epi::Params &p, hi
     sh.K = g.K;
     sh.lda = g.lda;
     sh.ldb = g.ldb;
-    sh.k_per_split = g.K;
+    sh.k_per_split = kps;
     sh.tiles_m = g.M / 256;
     sh.tiles_n = g.N / 256;
-    const dim3 grid(sh.tiles_m * sh.tiles_n);
+    sh.mv = g.mv ? g.mv : g.M;
+    sh.nv = g.nv ? g.nv : g.N;
+    const dim3 grid(sh.tiles_m * sh.tiles_n, splits);
     const half_t *A = reinterpret_cast<const half_t *>(g.A);
     const half_t *B = reinterpret_cast<const half_t *>(g.B);
-    hipLaunchKernelGGL((gemm_dma_kernel<Epi, AK, BK_, NW>), grid, dim3(DmaCfg<NW>::NT), 0, s, sh, A, B, p);
+    if (dma_full_epilogue(g))
+        hipLaunchKernelGGL((gemm_dma_kernel<Epi, AK, BK_, NW, false>), grid, dim3(DmaCfg<NW>::NT), 0, s, sh, A, B,
+                           p);
+    else
+        hipLaunchKernelGGL((gemm_dma_kernel<Epi, AK, BK_, NW, true>), grid, dim3(DmaCfg<NW>::NT), 0, s, sh, A, B,
+                           p);
     return hipGetLastError();
 }
 
-static hipError_t dispatch_dma(const GemmLaunch &g, hipStream_t s) {
+hipError_t launch_gemm_dma(const GemmLaunch &g, hipStream_t s) {
+    if (!gemm_dma_shape_ok(g)) return hipErrorInvalidValue;
+    // split-K: slices of k_per_split (a multiple of 128), the last one possibly shorter
+    const uint32_t splits_req = g.splits ? g.splits : 1;
+    const uint32_t kps = ((g.K / splits_req + 127) / 128) * 128;
+    const uint32_t splits = (g.K + kps - 1) / kps;
+    if (splits > 1 && g.op != Op::DwPartial) return hipErrorInvalidValue;
     const bool kk = g.a_kcontig && g.b_kcontig;
     switch (g.op) {
     case Op::Fwd:
-        return kk ? run_dma<EpiFwdK<half_t>, true, true>(g, g.fwd, s)
-                  : run_dma<EpiFwdK<half_t>, true, false>(g, g.fwd, s);
-    case Op::Hidden: return run_dma<EpiHiddenK<half_t>, true, true>(g, g.hid, s);
-    case Op::InputGrad: return run_dma<EpiStoreK, true, true>(g, g.st, s);
+        return kk ? run_dma<EpiFwdK<half_t>, true, true>(g, g.fwd, splits, kps, s)
+                  : run_dma<EpiFwdK<half_t>, true, false>(g, g.fwd, splits, kps, s);
+    case Op::InputGrad: return run_dma<EpiStoreK, true, true>(g, g.st, splits, kps, s);
     case Op::DwPartial:
-        return kk ? run_dma<EpiStoreK, true, true>(g, g.st, s) : run_dma<EpiStoreK, false, false>(g, g.st, s);
+        return kk ? run_dma<EpiStoreK, true, true>(g, g.st, splits, kps, s)
+                  : run_dma<EpiStoreK, false, false>(g, g.st, splits, kps, s);
     case Op::DwOpt:
-        return kk ? run_dma<EpiOptK<half_t>, true, true>(g, g.opt, s)
-                  : run_dma<EpiOptK<half_t>, false, false>(g, g.opt, s);
+        return kk ? run_dma<EpiOptK<half_t>, true, true>(g, g.opt, splits, kps, s)
+                  : run_dma<EpiOptK<half_t>, false, false>(g, g.opt, splits, kps, s);
     }
     return hipErrorInvalidValue;
 }
 
+// Split-K slices launch_gemm_dma makes of K for `splits` requested.
+uint32_t gemm_dma_splits(uint32_t K, uint32_t splits) {
+    const uint32_t kps = ((K / (splits ? splits : 1) + 127) / 128) * 128;
+    return (K + kps - 1) / kps;
+}
+
 hipError_t launch_gemm(const GemmLaunch &g, hipStream_t s) {
     if (g.M == 0 || g.N == 0) return hipSuccess;
+    if (gemm_direct_ok(g)) return launch_gemm_dma(g, s);
     if (g.dtype == 1) {
-        if (gemm_large_tile(g.dtype, g.M, g.N) && dma_ok(g)) return dispatch_dma(g, s);
         if (gemm_large_tile(g.dtype, g.M, g.N) && g.a_kcontig && g.b_kcontig) return dispatch_kk<CfgH256w8>(g, s);
         return dispatch_op<CfgH128>(g, s);
     }

@@ -200,7 +200,12 @@ template <int NW, int NF> struct OpN {
 template <bool KC, int NW, int NF> struct DmaOpSel { typedef OpK<NW, NF> type; };
 template <int NW, int NF> struct DmaOpSel<false, NW, NF> { typedef OpN<NW, NF> type; };
 
-template <class Epi, bool A_KC, bool B_KC, int NW>
+// Grid: (tiles, splits).  Split y reduces k in [y k_per_split, (y + 1) k_per_split)
+// (k_per_split a multiple of 128; the last split may be shorter, also a
+// multiple of 128).  EDGE: the operands are zero-padded copies whose M, N
+// extend past the real output [mv x nv]; the epilogue then goes element by
+// element through Epi::apply with those bounds (any leading dimension).
+template <class Epi, bool A_KC, bool B_KC, int NW, bool EDGE>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4)))
     gemm_dma_kernel(GemmShape sh, const half_t *__restrict__ A, const half_t *__restrict__ B,
                     typename Epi::Params ep) {
@@ -228,7 +233,10 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
     uint32_t tm, tn;
     tile_coords(blockIdx.x, sh.tiles_m, sh.tiles_n, tm, tn);
     const uint32_t m0 = tm * C::BM, n0 = tn * C::BN;
-    const int nk = (int)(sh.K / C::BK);
+    const uint32_t split = blockIdx.y;
+    const uint32_t kbeg = split * sh.k_per_split;
+    const int kb = (int)(kbeg / C::BK);                                  // first k-tile of this split
+    const int nk = (int)((min(sh.K, kbeg + sh.k_per_split) - kbeg) / C::BK);
 
     const uint32_t lds0 = (uint32_t)(uintptr_t)lsm;   // LDS byte address of smem
     OA oa;
@@ -267,13 +275,13 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
     };
 
     // prologue: tile 0 resident, tile 1 in flight, first fragments read
-    issue(0, 0);
+    issue(kb, 0);
     wait_vmcnt<0>();
     __builtin_amdgcn_s_barrier();
-    issue(nk > 1 ? 1 : 0, 1);
+    issue(kb + (nk > 1 ? 1 : 0), 1);
     read(0, 0, 0);
 
-    const int klast = nk - 1;
+    const int klast = kb + nk - 1;
     for (int kt0 = 0; kt0 < nk; kt0 += 2) {
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
@@ -288,7 +296,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
             wait_lgkmcnt<0>();                  // set 1 (k-step 3) is in registers
             wait_vmcnt<0>();                    // this wave's DMA of tile kt+1 landed
             __builtin_amdgcn_s_barrier();       // everyone's landed; stage s fully read
-            issue(min(kt + 2, klast), s);
+            issue(min(kb + kt + 2, klast), s);
             read(0, s ^ 1, 0);
             mma(1);
         }
@@ -311,7 +319,11 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
     static_assert(C::BN / 4 == 64, "one wave per 256-column row");
     float *E = reinterpret_cast<float *>(smem);
     const uint32_t c = lane * 4u;
-    const typename Epi::Col col = Epi::column(ep, n0 + c);
+    GemmShape shv = sh;   // EDGE: bounds of the real output
+    shv.M = sh.mv;
+    shv.N = sh.nv;
+    const typename Epi::Params eps = Epi::at_split(ep, split);
+    const typename Epi::Col col = EDGE ? typename Epi::Col{} : Epi::column(eps, n0 + c);
 #pragma unroll
     for (int pass = 0; pass < C::MT / MTP; ++pass) {
 #pragma unroll
@@ -329,6 +341,18 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
                 }
         }
         lds_barrier();
+        if constexpr (EDGE) {
+#pragma unroll 1
+            for (int b = 0; b < ROWS_PER_THREAD; ++b) {
+                const uint32_t r = wave + (uint32_t)NW * b;
+                const uint32_t wmi = r / (MTP * 32), rr = r % (MTP * 32);
+                const uint32_t m = m0 + wmi * C::TWM + pass * MTP * 32 + rr;
+                const floatx4 v = *reinterpret_cast<const floatx4 *>(E + r * EPITCH + c);
+                Epi::apply(ep, shv, m, n0 + c, v, split);
+            }
+            if (pass + 1 < C::MT / MTP) lds_barrier();
+            continue;
+        }
 #pragma unroll 1
         for (int b = 0; b < ROWS_PER_THREAD; b += EPI_BATCH) {
             typename Epi::Pre pre[EPI_BATCH];
@@ -339,13 +363,13 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
                 const uint32_t r = wave + (uint32_t)NW * (b + u);
                 const uint32_t wmi = r / (MTP * 32), rr = r % (MTP * 32);
                 mrow[u] = m0 + wmi * C::TWM + pass * MTP * 32 + rr;
-                Epi::load(ep, (uint64_t)mrow[u] * Epi::ldc(ep) + n0 + c, mrow[u], pre[u]);
+                Epi::load(eps, (uint64_t)mrow[u] * Epi::ldc(eps) + n0 + c, mrow[u], pre[u]);
             }
 #pragma unroll
             for (int u = 0; u < EPI_BATCH; ++u) {
                 const uint32_t r = wave + (uint32_t)NW * (b + u);
                 const floatx4 v = *reinterpret_cast<const floatx4 *>(E + r * EPITCH + c);
-                Epi::finish(ep, (uint64_t)mrow[u] * Epi::ldc(ep) + n0 + c, mrow[u], n0 + c, v, col, pre[u]);
+                Epi::finish(eps, (uint64_t)mrow[u] * Epi::ldc(eps) + n0 + c, mrow[u], n0 + c, v, col, pre[u]);
             }
         }
         if (pass + 1 < C::MT / MTP) lds_barrier();   // E is rewritten by the next pass

@@ -22,17 +22,6 @@ struct FwdEpi {
     uint32_t ldc, pad;
 };
 
-// Hidden error (backward.cu:79-100 / backward_wmma.cu:304-331).
-struct HiddenEpi {
-    const void *predrop, *preact, *mask, *norm_rstd, *centered, *prenorm;   // T
-    const float *nw;                                                        // master norm_w
-    float *grad, *d_prenorm, *d_norm_w, *d_norm_b;
-    half_t *d_prenorm_h;
-    uint32_t norm, act;
-    float leaky, inv_n, inv_m, loss_scale;
-    uint32_t ldc, pad;
-};
-
 // dW + optimiser on W (backward.cu:180-186 + 227-233).
 struct OptEpi {
     float *master;        // fp32 master (the parameter itself for fp32 blocks)
@@ -50,7 +39,7 @@ struct StoreEpi {
     uint32_t ldc, pad;
 };
 
-enum class Op { Fwd, Hidden, InputGrad, DwOpt, DwPartial };
+enum class Op { Fwd, InputGrad, DwOpt, DwPartial };
 
 // One GEMM launch.  dtype selects fp16 (MFMA 32x32x16 f16) or fp32
 // (MFMA 32x32x2 f32).  a_kcontig / b_kcontig as in gemm.h.
@@ -60,14 +49,22 @@ struct GemmLaunch {
     bool a_kcontig, b_kcontig;
     const void *A, *B;
     uint32_t splits;      // split-K factor (DwPartial only; 1 otherwise)
+    uint32_t mv, nv;      // real output extent when A / B are zero-padded copies (0 = M, N)
     Op op;
     FwdEpi fwd;
-    HiddenEpi hid;
     OptEpi opt;
     StoreEpi st;
 };
 
 hipError_t launch_gemm(const GemmLaunch &g, hipStream_t stream);
+// The 256x256 direct-to-LDS kernel on operands that fit it (gemm_dma_shape_ok):
+// M, N whole 256 tiles (zero-padded copies allowed: the epilogue stops at mv, nv),
+// K a multiple of 128; DwPartial may split K into g.splits slices.
+hipError_t launch_gemm_dma(const GemmLaunch &g, hipStream_t stream);
+bool gemm_dma_shape_ok(const GemmLaunch &g);
+bool gemm_dma_enabled();
+// Number of split-K slices launch_gemm_dma makes when asked for `splits`.
+uint32_t gemm_dma_splits(uint32_t K, uint32_t splits);
 // Number of output tiles the launcher would use (for split-K sizing).
 uint32_t gemm_tiles(uint32_t dtype, uint32_t M, uint32_t N);
 // True when an fp16 GEMM of this output size uses the 256x256 tile (k-contiguous operands only).
@@ -104,11 +101,9 @@ struct ErrArgs {
     half_t *d_prenorm_h;
 };
 // Both also write the column sums of d_prenorm / dNorm_w / dNorm_b over the
-// rows into partials [splits x 3 x n] when partials is non-null and the
-// vectorised kernel applies (n % 4 == 0, 16-byte aligned buffers); *sums
-// tells whether they did.
-hipError_t launch_output_error(const ErrArgs &a, float *partials, uint32_t splits, bool *sums, hipStream_t s);
-hipError_t launch_error_from_sum(const ErrArgs &a, float *partials, uint32_t splits, bool *sums, hipStream_t s);
+// rows into partials [splits x 3 x n] (splits from err_col_splits).
+hipError_t launch_output_error(const ErrArgs &a, float *partials, uint32_t splits, hipStream_t s);
+hipError_t launch_error_from_sum(const ErrArgs &a, float *partials, uint32_t splits, hipStream_t s);
 // Row splits the error kernels use for their column sums.
 uint32_t err_col_splits(uint32_t rows, uint32_t n);
 
@@ -133,14 +128,18 @@ hipError_t launch_vec_opt(const VecOptArgs &a, hipStream_t s);
 // Split-K dW reduction + W optimiser.
 struct DwReduceArgs {
     uint32_t dtype, rows, n, splits;
-    const float *partials;         // [splits][rows * n]
+    const float *partials;         // split sp, element (r, c) at sp * plane + r * pld + c
+    uint64_t plane;
+    uint32_t pld, pad;
     OptEpi e;
 };
 hipError_t launch_dw_reduce_opt(const DwReduceArgs &a, hipStream_t s);
 
 // fp16 transpose: out [cols x rows] (ld_out) = in [rows x cols] (ld_in)^T.
 // rows, cols, ld_in, ld_out multiples of 8; both buffers 16-byte aligned.
-hipError_t launch_transpose_h(const void *in, void *out, uint32_t rows, uint32_t cols, uint32_t ld_in,
-                              uint32_t ld_out, hipStream_t s);
+// Zero-padded fp16 copy: out [rows_p x cols_p] (cols_p % 8 == 0, 16-byte aligned)
+// holds in [rows x cols] (leading dim ld) and zeros elsewhere.
+hipError_t launch_pad_h(const void *in, uint32_t rows, uint32_t cols, uint32_t ld, void *out, uint32_t rows_p,
+                        uint32_t cols_p, hipStream_t s);
 
 }  // namespace skl

@@ -207,8 +207,10 @@ GemmPlan plan_gemm(const GemmLaunch &g) {
     return p;
 }
 
-// Runs g as planned; ws holds plan.bytes() of workspace.
-int32_t exec_gemm(skl_ctx *ctx, GemmLaunch g, const GemmPlan &p, char *ws) {
+// Runs g as planned; ws holds plan.bytes() of workspace.  full_out: the output
+// buffer has room for the padded grid (p.Mp x p.Np at its ldc), so the kernel
+// may write all of it (rows and columns past M, N come out zero).
+int32_t exec_gemm(skl_ctx *ctx, GemmLaunch g, const GemmPlan &p, char *ws, bool full_out = false) {
     char *wa = ws, *wb = ws + p.a_bytes, *wpart = ws + p.a_bytes + p.b_bytes;
     const OptEpi oe = g.opt;
     const uint32_t M = g.M, N = g.N;
@@ -229,8 +231,8 @@ int32_t exec_gemm(skl_ctx *ctx, GemmLaunch g, const GemmPlan &p, char *ws) {
             g.B = wb;
             g.ldb = g.b_kcontig ? p.Kp : p.Np;
         }
-        g.mv = M;
-        g.nv = N;
+        g.mv = full_out ? p.Mp : M;
+        g.nv = full_out ? p.Np : N;
         g.M = p.Mp;
         g.N = p.Np;
         g.K = p.Kp;
@@ -642,13 +644,15 @@ static int32_t hidden_error_impl(skl_ctx *ctx, const skl_dense_desc *cur, const 
     g.B = next->w;
     g.splits = 1;
     g.op = Op::InputGrad;
-    const size_t s_bytes = ((size_t)batch * cur->outputs * sizeof(float) + 255) & ~(size_t)255;
     const GemmPlan plan = plan_gemm(g);
+    // s on the kernel's whole (padded) grid: the full-tile epilogue, 16-byte rows
+    const uint32_t s_ld = plan.Np;
+    const size_t s_bytes = ((size_t)plan.Mp * s_ld * sizeof(float) + 255) & ~(size_t)255;
     if ((r = ensure_ws(ctx, s_bytes + plan.bytes()))) return r;
     float *sum = reinterpret_cast<float *>(ctx->ws);
     g.st.out = sum;
-    g.st.ldc = cur->outputs;
-    if ((r = exec_gemm(ctx, g, plan, reinterpret_cast<char *>(ctx->ws) + s_bytes))) return r;
+    g.st.ldc = s_ld;
+    if ((r = exec_gemm(ctx, g, plan, reinterpret_cast<char *>(ctx->ws) + s_bytes, true))) return r;
 
     // ... then act' * mask and the element-local norm gradient (backward.cu:79-100), with
     // the column sums of d_prenorm / dNorm for cur's backward
@@ -663,6 +667,7 @@ static int32_t hidden_error_impl(skl_ctx *ctx, const skl_dense_desc *cur, const 
     a.inv_m = 1.0f / (float)batch;
     a.loss_scale = 1.0f;
     a.s = sum;
+    a.s_ld = s_ld;
     a.predrop = cur->predrop;
     a.preact = cur->preact;
     a.mask = cur->mask;

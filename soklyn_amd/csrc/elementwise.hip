@@ -159,6 +159,123 @@ template <typename T> __global__ void __launch_bounds__(256) norm_rows_kernel(Ro
     }
 }
 
+// The same with the row held in registers: each element of prenorm is read
+// once, and every cache write is a 16-byte store when rows are 16-byte aligned
+// (VEC: a thread owns chunks of VW consecutive elements, chunk t + 256 i) or
+// a coalesced element store otherwise (a thread owns elements t + 256 i).
+// PER = chunks (VEC) or elements per thread; rows up to 256 x PER (x VW).
+template <typename T, bool VEC, int PER> __global__ void __launch_bounds__(256) norm_rows_reg_kernel(RowNormArgs a) {
+    constexpr int VW = VEC ? 16 / (int)sizeof(T) : 1;
+    constexpr int E = PER * VW;   // elements per thread
+    __shared__ float red[4];
+    const uint32_t row = blockIdx.x;
+    const uint32_t n = a.n;
+    const uint64_t base = (uint64_t)row * n;
+    const T *pz = reinterpret_cast<const T *>(a.prenorm) + base;
+    float z[E];
+    bool in[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const uint32_t c0 = (threadIdx.x + 256u * i) * VW;
+        in[i] = c0 < n;
+        if constexpr (VEC) {
+            T v[VW];
+            if (in[i]) {
+                *reinterpret_cast<u32x4_t *>(v) = *reinterpret_cast<const u32x4_t *>(pz + c0);
+            } else {
+#pragma unroll
+                for (int e = 0; e < VW; ++e) v[e] = (T)0;
+            }
+#pragma unroll
+            for (int e = 0; e < VW; ++e) z[i * VW + e] = to_f32(v[e]);
+        } else {
+            z[i] = in[i] ? to_f32(pz[c0]) : 0.0f;
+        }
+    }
+    float mean = 0.0f, rstd32;
+    T rstd_t;
+    if (a.norm == 1) {
+        float sq = 0.0f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) sq = fmaf(z[e], z[e], sq);
+        sq = block_sum256(sq, red);
+        rstd32 = 1.0f / sqrtf(sq / (float)n + 1e-6f);
+        rstd_t = from_f32<T>(rstd32);
+    } else {
+        float sm = 0.0f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) sm += z[e];
+        mean = block_sum256(sm, red) / (float)n;
+        float ss = 0.0f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            // padding elements (z = 0) are not part of the row
+            const uint32_t c = VEC ? (threadIdx.x + 256u * (e / VW)) * VW + e % VW : threadIdx.x + 256u * e;
+            const float v = c < n ? z[e] - mean : 0.0f;
+            ss = fmaf(v, v, ss);
+        }
+        ss = block_sum256(ss, red);
+        rstd32 = 1.0f / sqrtf(ss / (float)n + 1e-6f);
+        rstd_t = from_f32<T>(rstd32);
+    }
+    if (threadIdx.x == 0) stv<T>(a.norm_rstd, row, rstd_t);
+    const float scale = a.use_dropout ? 1.0f / (1.0f - a.p) : 1.0f;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        if (!in[i]) continue;
+        const uint32_t c0 = (threadIdx.x + 256u * i) * VW;
+        T cen[VW], pre[VW], pd[VW], mk[VW], ot[VW], g[VW], bb[VW];
+        if constexpr (VEC) {
+            *reinterpret_cast<u32x4_t *>(g) = *reinterpret_cast<const u32x4_t *>(reinterpret_cast<const T *>(a.norm_w) + c0);
+            if (a.norm == 2)
+                *reinterpret_cast<u32x4_t *>(bb) =
+                    *reinterpret_cast<const u32x4_t *>(reinterpret_cast<const T *>(a.norm_b) + c0);
+        } else {
+            g[0] = ldv<T>(a.norm_w, c0);
+            if (a.norm == 2) bb[0] = ldv<T>(a.norm_b, c0);
+        }
+#pragma unroll
+        for (int e = 0; e < VW; ++e) {
+            const float zv = z[i * VW + e];
+            T p;
+            if (a.norm == 1) {
+                // T arithmetic: (prenorm * rstd) * norm_w, each product rounded to T (forward.cu:61-72)
+                cen[e] = from_f32<T>(zv);
+                p = from_f32<T>(to_f32(from_f32<T>(zv * to_f32(rstd_t))) * to_f32(g[e]));
+            } else {
+                const float v = zv - mean;
+                cen[e] = from_f32<T>(v);
+                p = from_f32<T>(fmaf(v * rstd32, to_f32(g[e]), to_f32(bb[e])));
+            }
+            pre[e] = p;
+            const float act = activation(a.act, to_f32(p), a.leaky);
+            pd[e] = from_f32<T>(act);
+            if (a.use_dropout) {
+                const bool keep = dropout_u(c0 + e, row, a.seed + row * 7u) >= a.p;
+                mk[e] = keep ? from_f32<T>(scale) : (T)0;
+                ot[e] = keep ? from_f32<T>(act * scale) : (T)0;
+            } else {
+                ot[e] = pd[e];
+            }
+        }
+        const uint64_t idx = base + c0;
+        if constexpr (VEC) {
+            *reinterpret_cast<u32x4_t *>(reinterpret_cast<T *>(a.centered) + idx) = *reinterpret_cast<u32x4_t *>(cen);
+            *reinterpret_cast<u32x4_t *>(reinterpret_cast<T *>(a.preact) + idx) = *reinterpret_cast<u32x4_t *>(pre);
+            *reinterpret_cast<u32x4_t *>(reinterpret_cast<T *>(a.predrop) + idx) = *reinterpret_cast<u32x4_t *>(pd);
+            *reinterpret_cast<u32x4_t *>(reinterpret_cast<T *>(a.out) + idx) = *reinterpret_cast<u32x4_t *>(ot);
+            if (a.use_dropout)
+                *reinterpret_cast<u32x4_t *>(reinterpret_cast<T *>(a.mask) + idx) = *reinterpret_cast<u32x4_t *>(mk);
+        } else {
+            stv<T>(a.centered, idx, cen[0]);
+            stv<T>(a.preact, idx, pre[0]);
+            stv<T>(a.predrop, idx, pd[0]);
+            stv<T>(a.out, idx, ot[0]);
+            if (a.use_dropout) stv<T>(a.mask, idx, mk[0]);
+        }
+    }
+}
+
 // BatchNorm: one thread per column over the batch rows (forward.cu:74-126 with
 // norm == 3), then act + dropout.  Consecutive threads read consecutive columns.
 template <typename T> __global__ void __launch_bounds__(256) norm_cols_kernel(RowNormArgs a) {
@@ -187,6 +304,30 @@ template <typename T> __global__ void __launch_bounds__(256) norm_cols_kernel(Ro
     }
 }
 
+static bool a16p(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Rows up to 256 x 16 elements run with the row in registers; longer rows take
+// the looping kernel.
+template <typename T> static void launch_norm_rows(const RowNormArgs &a, hipStream_t s) {
+    constexpr uint32_t VW = 16 / sizeof(T);
+    const bool vec = a.n % VW == 0 && a16p(a.prenorm) && a16p(a.norm_w) && (a.norm != 2 || a16p(a.norm_b)) &&
+                     a16p(a.centered) && a16p(a.preact) && a16p(a.predrop) && a16p(a.out) &&
+                     (!a.use_dropout || a16p(a.mask));
+    const dim3 g(a.m), b(256);
+    if (vec && a.n <= 256 * VW)
+        hipLaunchKernelGGL((norm_rows_reg_kernel<T, true, 1>), g, b, 0, s, a);
+    else if (vec && a.n <= 2 * 256 * VW)
+        hipLaunchKernelGGL((norm_rows_reg_kernel<T, true, 2>), g, b, 0, s, a);
+    else if (a.n <= 256 * 4)
+        hipLaunchKernelGGL((norm_rows_reg_kernel<T, false, 4>), g, b, 0, s, a);
+    else if (a.n <= 256 * 8)
+        hipLaunchKernelGGL((norm_rows_reg_kernel<T, false, 8>), g, b, 0, s, a);
+    else if (a.n <= 256 * 16)
+        hipLaunchKernelGGL((norm_rows_reg_kernel<T, false, 16>), g, b, 0, s, a);
+    else
+        hipLaunchKernelGGL(norm_rows_kernel<T>, g, b, 0, s, a);
+}
+
 hipError_t launch_norm_act(const RowNormArgs &a, hipStream_t s) {
     if (a.m == 0 || a.n == 0) return hipSuccess;
     if (a.norm == 3) {
@@ -194,11 +335,10 @@ hipError_t launch_norm_act(const RowNormArgs &a, hipStream_t s) {
             hipLaunchKernelGGL(norm_cols_kernel<half_t>, dim3(cdiv(a.n, 256)), dim3(256), 0, s, a);
         else
             hipLaunchKernelGGL(norm_cols_kernel<float>, dim3(cdiv(a.n, 256)), dim3(256), 0, s, a);
+    } else if (a.dtype == 1) {
+        launch_norm_rows<half_t>(a, s);
     } else {
-        if (a.dtype == 1)
-            hipLaunchKernelGGL(norm_rows_kernel<half_t>, dim3(a.m), dim3(256), 0, s, a);
-        else
-            hipLaunchKernelGGL(norm_rows_kernel<float>, dim3(a.m), dim3(256), 0, s, a);
+        launch_norm_rows<float>(a, s);
     }
     return hipGetLastError();
 }
@@ -351,12 +491,15 @@ __device__ __forceinline__ f32x4 output_err4(const ErrArgs &a, uint64_t idx, uin
 // measured on the C3 step (rows x column groups per thread in {4x1, 2x2, 1x4,
 // 2x4}, 512 to 2048 workgroups) the fastest, both alone and between the GEMMs.
 constexpr int ERR_UR = 4;
+// Without VEC a thread owns one column (cnt = 1) instead: consecutive lanes
+// read consecutive elements, whatever the rows' alignment.
 template <typename T, bool FROM_SUM, bool VEC>
 __global__ void __launch_bounds__(256) error_cols_kernel(ErrArgs a, float *__restrict__ partials, uint32_t per) {
     typedef Grp<T, VEC> G;
-    const uint32_t c = blockIdx.x * 1024 + threadIdx.x * 4;
+    const uint32_t c = VEC ? blockIdx.x * 1024 + threadIdx.x * 4 : blockIdx.x * 256 + threadIdx.x;
     if (c >= a.n) return;
-    const uint32_t cnt = min(4u, a.n - c);
+    const uint32_t cnt = VEC ? min(4u, a.n - c) : 1u;
+    const uint32_t s_ld = a.s_ld ? a.s_ld : a.n;
     const uint32_t r0 = blockIdx.y * per;
     const uint32_t r1 = min(a.rows, r0 + per);
     f32x4 sdp = {0, 0, 0, 0}, snw = {0, 0, 0, 0}, snb = {0, 0, 0, 0};
@@ -367,7 +510,7 @@ __global__ void __launch_bounds__(256) error_cols_kernel(ErrArgs a, float *__res
             for (int u = 0; u < ERR_UR; ++u) {
                 if (rb + u >= r1) break;
                 const uint64_t idx = (uint64_t)(rb + u) * a.n + c;
-                x0[u] = G::ldf(a.s, idx, cnt, true);
+                x0[u] = G::ldf(a.s, (uint64_t)(rb + u) * s_ld + c, cnt, true);
                 x1[u] = G::ld(a.predrop, idx, cnt);
                 x2[u] = G::ld(a.preact, idx, cnt);
                 x3[u] = G::ld(a.mask, idx, cnt);
@@ -403,7 +546,7 @@ __global__ void __launch_bounds__(256) error_cols_kernel(ErrArgs a, float *__res
 static bool a16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 static bool err_vec_ok(const ErrArgs &a, bool from_sum, const float *partials) {
-    if ((a.n & 3u) != 0) return false;
+    if ((a.n & 3u) != 0 || (from_sum && (a.s_ld & 3u) != 0)) return false;
     const void *ptrs[] = {a.grad, a.d_prenorm, a.d_prenorm_h, a.preact, a.norm ? a.nw : nullptr,
                           a.norm ? a.d_norm_w : nullptr, a.norm ? a.d_norm_b : nullptr,
                           a.norm == 1 ? a.prenorm : nullptr, a.norm >= 2 ? a.centered : nullptr,
@@ -427,11 +570,12 @@ uint32_t err_col_splits(uint32_t rows, uint32_t n) {
 template <bool FROM_SUM, typename T>
 static void launch_error_t(const ErrArgs &a, float *partials, uint32_t splits, hipStream_t s) {
     const uint32_t per = cdiv(a.rows, splits);
-    const dim3 g(cdiv(a.n, 1024), splits);
     if (err_vec_ok(a, FROM_SUM, partials))
-        hipLaunchKernelGGL((error_cols_kernel<T, FROM_SUM, true>), g, dim3(256), 0, s, a, partials, per);
+        hipLaunchKernelGGL((error_cols_kernel<T, FROM_SUM, true>), dim3(cdiv(a.n, 1024), splits), dim3(256), 0, s,
+                           a, partials, per);
     else
-        hipLaunchKernelGGL((error_cols_kernel<T, FROM_SUM, false>), g, dim3(256), 0, s, a, partials, per);
+        hipLaunchKernelGGL((error_cols_kernel<T, FROM_SUM, false>), dim3(cdiv(a.n, 256), splits), dim3(256), 0, s,
+                           a, partials, per);
 }
 
 hipError_t launch_output_error(const ErrArgs &a, float *partials, uint32_t splits, hipStream_t s) {
@@ -600,21 +744,38 @@ hipError_t launch_dw_reduce_opt(const DwReduceArgs &a, hipStream_t s) {
 // ---- zero-padded fp16 copy (operand staging for the 256x256 GEMM) -----------------------
 // out[r][c] = (r < rows && c < cols) ? in[r ld + c] : 0 for r < rows_p, c < cols_p
 // (cols_p a multiple of 8): a thread writes 8 consecutive halves (16 bytes).
+// chunks (16-byte aligned source base): a source window that is not 16-byte
+// aligned is cut out of the two aligned 16-byte chunks covering it (funnel
+// shifts), as long as both lie inside the source's readable elements; element
+// loads otherwise.
 __global__ void __launch_bounds__(256) pad_h_kernel(const half_t *__restrict__ in, uint32_t rows, uint32_t cols,
                                                     uint32_t ld, half_t *__restrict__ out, uint32_t rows_p,
-                                                    uint32_t cols_p, uint32_t vec_in) {
+                                                    uint32_t cols_p, uint32_t chunks) {
     const uint32_t gpr = cols_p / 8;
     const uint64_t total = (uint64_t)rows_p * gpr;
+    const uint64_t in_elems = rows ? (uint64_t)(rows - 1) * ld + cols : 0;   // readable source elements
     for (uint64_t q = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; q < total;
          q += (uint64_t)gridDim.x * blockDim.x) {
         const uint32_t r = (uint32_t)(q / gpr), c = (uint32_t)(q % gpr) * 8;
         u32x4_t v = {0, 0, 0, 0};
         if (r < rows && c < cols) {
-            const half_t *src = in + (uint64_t)r * ld + c;
-            if (vec_in && c + 8 <= cols) {
-                v = *reinterpret_cast<const u32x4_t *>(src);
+            const uint64_t e0 = (uint64_t)r * ld + c;            // first source element
+            const uint64_t a0 = e0 & ~(uint64_t)7;                // its aligned chunk
+            const uint32_t sh = (uint32_t)(e0 - a0) * 2;           // byte offset within it
+            if (chunks && c + 8 <= cols && a0 + (sh ? 16 : 8) <= in_elems) {
+                const u32x4_t lo = *reinterpret_cast<const u32x4_t *>(in + a0);
+                const u32x4_t hi = sh ? *reinterpret_cast<const u32x4_t *>(in + a0 + 8) : lo;
+                const uint32_t w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+                const uint32_t wd = sh >> 2, bits = (sh & 3u) * 8u;   // whole dwords, then 0 or 16 bits
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    const uint32_t x0 = wd == 0 ? w[d] : wd == 1 ? w[d + 1] : wd == 2 ? w[d + 2] : w[d + 3];
+                    const uint32_t x1 = wd == 0 ? w[d + 1] : wd == 1 ? w[d + 2] : wd == 2 ? w[d + 3] : w[d + 4];
+                    v[d] = __builtin_amdgcn_alignbit(x1, x0, bits);   // (x1:x0) >> bits
+                }
             } else {
                 half_t h[8];
+                const half_t *src = in + e0;
 #pragma unroll
                 for (uint32_t e = 0; e < 8; ++e) h[e] = c + e < cols ? src[e] : (half_t)0;
                 v = __builtin_bit_cast(u32x4_t, h);
@@ -629,9 +790,8 @@ hipError_t launch_pad_h(const void *in, uint32_t rows, uint32_t cols, uint32_t l
     if (cols_p % 8 || rows_p < rows || cols_p < cols || !a16(out)) return hipErrorInvalidValue;
     const uint64_t groups = (uint64_t)rows_p * (cols_p / 8);
     if (groups == 0) return hipSuccess;
-    const uint32_t vec_in = (ld % 8 == 0 && a16(in)) ? 1u : 0u;
     hipLaunchKernelGGL(pad_h_kernel, grid_for(groups, 256), dim3(256), 0, s, reinterpret_cast<const half_t *>(in),
-                       rows, cols, ld, reinterpret_cast<half_t *>(out), rows_p, cols_p, vec_in);
+                       rows, cols, ld, reinterpret_cast<half_t *>(out), rows_p, cols_p, a16(in) ? 1u : 0u);
     return hipGetLastError();
 }
 

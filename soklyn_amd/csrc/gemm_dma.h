@@ -342,13 +342,25 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
         }
         lds_barrier();
         if constexpr (EDGE) {
+            // element by element, lane l taking columns l, l + 64, l + 128, l + 192
+            // of the row: each store instruction covers 64 consecutive columns
+            // whatever the output's alignment (Epi::apply with the column bound
+            // lowered to n + 1 handles exactly column n)
 #pragma unroll 1
             for (int b = 0; b < ROWS_PER_THREAD; ++b) {
                 const uint32_t r = wave + (uint32_t)NW * b;
                 const uint32_t wmi = r / (MTP * 32), rr = r % (MTP * 32);
                 const uint32_t m = m0 + wmi * C::TWM + pass * MTP * 32 + rr;
-                const floatx4 v = *reinterpret_cast<const floatx4 *>(E + r * EPITCH + c);
-                Epi::apply(ep, shv, m, n0 + c, v, split);
+                if (m >= shv.M) continue;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const uint32_t n = n0 + lane + 64u * q;
+                    if (n >= shv.N) break;
+                    GemmShape one = shv;
+                    one.N = n + 1;
+                    const floatx4 v = {E[r * EPITCH + lane + 64u * q], 0.0f, 0.0f, 0.0f};
+                    Epi::apply(ep, one, m, n, v, split);
+                }
             }
             if (pass + 1 < C::MT / MTP) lds_barrier();
             continue;

@@ -94,6 +94,7 @@ struct ErrArgs {
     float leaky, inv_n, inv_m, loss_scale;
     const void *out, *preact, *target;                 // output error
     const float *s;                                    // error_from_sum
+    uint32_t s_ld, pad;                                // row pitch of s (0 = n)
     const void *predrop, *mask;                        // error_from_sum
     const void *norm_rstd, *centered, *prenorm;
     const float *nw;

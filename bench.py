@@ -202,10 +202,20 @@ def cpu_baseline_mlp(cfg, rows: int, reps: int = 3):
                       f"in fp32 on the oracle; median of {reps} passes after one warm-up, {dt:.2f} s per pass"}
 
 
+def timing_events(n):
+    """n (start, stop) pairs of timing events, each recorded once so its HIP event exists."""
+    import torch
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for a, b in evs:
+        a.record()
+        b.record()
+    return evs
+
+
 class BlockBench:
     """Single DenseBlock: forward -> error_from_sum -> backward -> input_grad."""
-    calls = ("forward_gemm", "error_elementwise", "dw_gemm_adam", "dx_gemm")
-    single_launch = ("forward_gemm", "dx_gemm")   # one GEMM kernel per call at these shapes
+    calls = ("forward", "error_from_sum", "backward", "input_grad")
+    gemms = ("forward_gemm", "dx_gemm")   # GEMM kernels timed alone (the roofline candidates)
 
     def __init__(self, cfg, ctx, stream):
         import torch
@@ -226,16 +236,20 @@ class BlockBench:
         self.step_no = 0
         self.flops = 3 * 2.0 * M * K * N
         self.kernel_flops = {"forward_gemm": 2.0 * M * K * N, "dx_gemm": 2.0 * M * K * N}
-        self.stream = stream
+        self.stream, self.ctx = stream, ctx
 
-    def step(self, ev=None):
+    def step(self, ev=None, gev=None):
         # ev: per-call (start, end) HIP events on the launch stream, recorded inside the
-        # timed steps so each call is timed in the step's own context
+        # timed steps so each call is timed in the step's own context; gev: events the
+        # library records around the GEMM kernel alone of the forward and dX calls
         self.step_no += 1
         b, M = self.blk, self.M
         fns = (lambda: b.forward(self.x, M), lambda: b.error_from_sum(self.dy, M),
                lambda: b.backward(self.x, self.tc, self.step_no), lambda: b.input_grad(M, self.dx))
+        gemm_of = {0: 0, 3: 1}
         for i, fn in enumerate(fns):
+            if gev is not None and i in gemm_of:
+                self.ctx.time_next_gemm(*gev[gemm_of[i]])
             if ev is not None:
                 ev[i][0].record(self.stream)
             fn()
@@ -265,15 +279,16 @@ class MlpBench:
         self.M, self.L = M, L
         self.step_no = 0
         self.flops = mlp_flops(dims, M)
-        # the roofline call: the hidden error of layer `timed_layer` (one GEMM launch with the
-        # act' / mask / norm-gradient epilogue), dX through the weights of the layer above it
+        # the roofline kernel: the GEMM of the hidden error of layer `timed_layer`, dX
+        # through the weights of the layer above it (the call also runs the error kernel)
         k = cfg["timed_layer"]
         self.timed = f"hidden_error_gemm_layer{k}"
-        self.calls = (self.timed,)
-        self.single_launch = (self.timed,)
+        self.calls = (f"hidden_error_layer{k}",)
+        self.gemms = (self.timed,)
         self.kernel_flops = {self.timed: 2.0 * M * dims[k + 1] * dims[k + 2]}
+        self.ctx = ctx
 
-    def step(self, ev=None):
+    def step(self, ev=None, gev=None):
         self.step_no += 1
         cfg, b, M, L = self.cfg, self.blocks, self.M, self.L
         seeds = dropout_seeds(cfg, self.step_no)
@@ -283,11 +298,13 @@ class MlpBench:
         b[L - 1].output_error(self.t, cfg["loss"], cfg["loss_act"])
         b[L - 1].backward(b[L - 2].out, self.tc, self.step_no)
         for i in range(L - 2, -1, -1):
-            timed = ev is not None and i == cfg["timed_layer"]
-            if timed:
+            timed = i == cfg["timed_layer"]
+            if timed and gev is not None:
+                self.ctx.time_next_gemm(*gev[0])
+            if timed and ev is not None:
                 ev[0][0].record(self.stream)
             b[i].hidden_error(b[i + 1], M)
-            if timed:
+            if timed and ev is not None:
                 ev[0][1].record(self.stream)
             b[i].backward(b[i - 1].out if i > 0 else self.x, self.tc, self.step_no)
 
@@ -312,29 +329,33 @@ def main():
     ctx.set_stream(stream.cuda_stream)
     ctx.set_sync(False)
     bench = BlockBench(cfg, ctx, stream) if cfg["kind"] == "block" else MlpBench(cfg, ctx, stream)
-    calls = bench.calls
+    calls, gemms = bench.calls, bench.gemms
 
     for _ in range(args.warmup):
         bench.step()
     torch.cuda.synchronize()
-    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in calls]
-           for _ in range(args.steps)]
+    evs = [timing_events(len(calls)) for _ in range(args.steps)]
+    gevs = [timing_events(len(gemms)) for _ in range(args.steps)]
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
     ev0.record(stream)
     for k in range(args.steps):
-        bench.step(evs[k])
+        bench.step(evs[k], gevs[k])
     ev1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms = ev0.elapsed_time(ev1) / args.steps
     value = bench.flops / (ms * 1e-3) / 1e12
-    # average duration of each timed call over the timed steps
-    kern = {c: sum(evs[k][i][0].elapsed_time(evs[k][i][1]) for k in range(args.steps)) / args.steps
-            for i, c in enumerate(calls)}
 
-    # The roofline kernel: the slowest single-launch GEMM call
-    dom = max(bench.single_launch, key=lambda k: kern[k])
+    def avg(table, names):
+        return {c: sum(table[k][i][0].elapsed_time(table[k][i][1]) for k in range(args.steps)) / args.steps
+                for i, c in enumerate(names)}
+    call_ms = avg(evs, calls)     # each hot-path call in the step
+    kern = avg(gevs, gemms)       # the GEMM kernels alone
+
+    # The roofline kernel: the slowest of the timed GEMM kernels
+    dom = max(gemms, key=lambda k: kern[k])
     achieved = bench.kernel_flops[dom] / (kern[dom] * 1e-3) / 1e12
     half = cfg.get("half", True)
     peak = PEAK["f16" if half else "f32"]
@@ -366,7 +387,8 @@ def main():
                      "frac": round(achieved / peak, 4),
                      "traffic": trec["bytes_per_launch"] if trec else None,
                      "traffic_source": trec["source"] if trec else None, "kernel": dom,
-                     "kernel_ms": {k: round(v, 4) for k, v in kern.items()}},
+                     "kernel_ms": {k: round(v, 4) for k, v in kern.items()},
+                     "call_ms": {k: round(v, 4) for k, v in call_ms.items()}},
     }
     if not args.no_cpu:
         if cfg["kind"] == "block":

@@ -72,6 +72,7 @@ _SIGS = {
     "skl_fill": (C.c_int32, [_VP, _VP, C.c_uint32, C.c_float, C.c_size_t]),
     "skl_cast": (C.c_int32, [_VP, _VP, C.c_uint32, _VP, C.c_uint32, C.c_size_t]),
     "skl_scramble_seed": (C.c_uint32, [C.c_uint32, C.c_uint32]),
+    "skl_ctx_time_next_gemm": (C.c_int32, [C.c_void_p, C.c_void_p, C.c_void_p]),
     "skl_dense_forward": (C.c_int32, [_VP, C.POINTER(SklDenseDesc), _VP, C.c_uint32, C.c_uint32, C.c_uint32,
                                       C.c_uint32, C.c_uint32]),
     "skl_dense_output_error": (C.c_int32, [_VP, C.POINTER(SklDenseDesc), _VP, C.c_uint32, C.c_uint32,
@@ -153,6 +154,10 @@ class Context:
 
     def set_stream(self, stream_ptr: int | None):
         call("skl_ctx_set_stream", self.h, C.c_void_p(stream_ptr) if stream_ptr else None)
+
+    def time_next_gemm(self, start, stop):
+        """Record two torch.cuda.Event objects around the GEMM kernel of the next hot-path call."""
+        call("skl_ctx_time_next_gemm", self.h, C.c_void_p(start.cuda_event), C.c_void_p(stop.cuda_event))
 
     def set_sync(self, sync: bool):
         call("skl_ctx_set_sync", self.h, int(sync))

@@ -40,6 +40,7 @@ struct skl_ctx {
     float *cols;         // ColSums storage
     size_t cols_bytes;
     ColSums cs;
+    hipEvent_t gemm_start, gemm_stop;   // skl_ctx_time_next_gemm
 };
 
 namespace {
@@ -207,6 +208,19 @@ GemmPlan plan_gemm(const GemmLaunch &g) {
     return p;
 }
 
+// One GEMM launch, bracketed by the events of skl_ctx_time_next_gemm when set.
+hipError_t timed_gemm(skl_ctx *ctx, const GemmLaunch &g, bool dma) {
+    hipEvent_t stop = ctx->gemm_stop;
+    if (ctx->gemm_start) {
+        const hipError_t e = hipEventRecord(ctx->gemm_start, ctx->stream);
+        ctx->gemm_start = ctx->gemm_stop = nullptr;
+        if (e != hipSuccess) return e;
+    }
+    const hipError_t e = dma ? launch_gemm_dma(g, ctx->stream) : launch_gemm(g, ctx->stream);
+    if (e != hipSuccess) return e;
+    return stop ? hipEventRecord(stop, ctx->stream) : hipSuccess;
+}
+
 // Runs g as planned; ws holds plan.bytes() of workspace.  full_out: the output
 // buffer has room for the padded grid (p.Mp x p.Np at its ldc), so the kernel
 // may write all of it (rows and columns past M, N come out zero).
@@ -246,7 +260,7 @@ int32_t exec_gemm(skl_ctx *ctx, GemmLaunch g, const GemmPlan &p, char *ws, bool 
             g.mv = g.M;
             g.nv = g.N;
         }
-        SKL_TRY(launch_gemm_dma(g, ctx->stream));
+        SKL_TRY(timed_gemm(ctx, g, true));
     } else {
         if (p.splits > 1) {
             g.op = Op::DwPartial;
@@ -255,7 +269,7 @@ int32_t exec_gemm(skl_ctx *ctx, GemmLaunch g, const GemmPlan &p, char *ws, bool 
             g.st.split_stride = (uint64_t)M * N;
             g.st.ldc = N;
         }
-        SKL_TRY(launch_gemm(g, ctx->stream));
+        SKL_TRY(timed_gemm(ctx, g, false));
     }
     if (p.splits > 1) {
         DwReduceArgs d{};
@@ -408,6 +422,14 @@ int32_t skl_ctx_destroy(skl_ctx *ctx) {
 int32_t skl_ctx_set_sync(skl_ctx *ctx, uint32_t sync_each_call) {
     if (!ctx) return SKL_ERR_NULL_POINTER;
     ctx->sync = sync_each_call ? 1 : 0;
+    return SKL_OK;
+}
+
+int32_t skl_ctx_time_next_gemm(skl_ctx *ctx, void *start_event, void *stop_event) {
+    if (!ctx) return SKL_ERR_NULL_POINTER;
+    if (!start_event != !stop_event) return SKL_ERR_NULL_POINTER;
+    ctx->gemm_start = reinterpret_cast<hipEvent_t>(start_event);
+    ctx->gemm_stop = reinterpret_cast<hipEvent_t>(stop_event);
     return SKL_OK;
 }
 

@@ -130,6 +130,7 @@ bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 //  * the register-staged kernels otherwise (fp32; small or skinny fp16), with
 //    the same split-K for small dW grids.
 struct GemmPlan {
+    bool skinny;               // N <= 16: the streaming kernels (forward, dW partials)
     bool dma;
     bool pad_a, pad_b;
     uint32_t Mp, Np, Kp;       // dims the kernel runs on
@@ -154,6 +155,15 @@ GemmPlan plan_gemm(const GemmLaunch &g) {
     p.Np = g.N;
     p.Kp = g.K;
     const bool dw = g.op == Op::DwOpt;
+    // skinny outputs: a stream over X beats any MFMA tile that is >90% padding
+    if (g.N <= 16 && g.M && g.K && ((g.op == Op::Fwd && skinny_fwd_ok(g)) || (dw && g.b32 && !g.a_kcontig))) {
+        p.skinny = true;
+        if (dw) {
+            p.splits = skinny_dw_slices(g.K, g.M);
+            p.part_bytes = (size_t)p.splits * g.M * 16 * sizeof(float);
+        }
+        return p;
+    }
     if (g.dtype == SKL_F16 && gemm_dma_enabled() && g.M && g.N && g.K) {
         const uint32_t Mp = round_up(g.M, 256), Np = round_up(g.N, 256), Kp = round_up(g.K, 128);
         const uint32_t tiles = (Mp / 256) * (Np / 256);
@@ -208,15 +218,24 @@ GemmPlan plan_gemm(const GemmLaunch &g) {
     return p;
 }
 
+enum class GemmKind { Dma, Staged, SkinnyFwd, SkinnyDw };
+
 // One GEMM launch, bracketed by the events of skl_ctx_time_next_gemm when set.
-hipError_t timed_gemm(skl_ctx *ctx, const GemmLaunch &g, bool dma) {
+hipError_t timed_gemm(skl_ctx *ctx, const GemmLaunch &g, GemmKind kind, float *partials = nullptr,
+                      uint32_t slices = 0) {
     hipEvent_t stop = ctx->gemm_stop;
     if (ctx->gemm_start) {
         const hipError_t e = hipEventRecord(ctx->gemm_start, ctx->stream);
         ctx->gemm_start = ctx->gemm_stop = nullptr;
         if (e != hipSuccess) return e;
     }
-    const hipError_t e = dma ? launch_gemm_dma(g, ctx->stream) : launch_gemm(g, ctx->stream);
+    hipError_t e = hipSuccess;
+    switch (kind) {
+    case GemmKind::Dma: e = launch_gemm_dma(g, ctx->stream); break;
+    case GemmKind::Staged: e = launch_gemm(g, ctx->stream); break;
+    case GemmKind::SkinnyFwd: e = launch_skinny_fwd(g, ctx->stream); break;
+    case GemmKind::SkinnyDw: e = launch_skinny_dw(g, partials, slices, ctx->stream); break;
+    }
     if (e != hipSuccess) return e;
     return stop ? hipEventRecord(stop, ctx->stream) : hipSuccess;
 }
@@ -228,6 +247,21 @@ int32_t exec_gemm(skl_ctx *ctx, GemmLaunch g, const GemmPlan &p, char *ws, bool 
     char *wa = ws, *wb = ws + p.a_bytes, *wpart = ws + p.a_bytes + p.b_bytes;
     const OptEpi oe = g.opt;
     const uint32_t M = g.M, N = g.N;
+    if (p.skinny) {
+        if (g.op == Op::Fwd) return hip_status(timed_gemm(ctx, g, GemmKind::SkinnyFwd));
+        SKL_TRY(timed_gemm(ctx, g, GemmKind::SkinnyDw, reinterpret_cast<float *>(wpart), p.splits));
+        DwReduceArgs d{};
+        d.dtype = g.dtype;
+        d.rows = M;
+        d.n = N;
+        d.splits = p.splits;
+        d.partials = reinterpret_cast<const float *>(wpart);
+        d.plane = (uint64_t)M * 16;
+        d.pld = 16;
+        d.e = oe;
+        SKL_TRY(launch_dw_reduce_opt(d, ctx->stream));
+        return SKL_OK;
+    }
     if (p.dma) {
         if (p.pad_a) {
             if (g.a_kcontig)
@@ -260,7 +294,7 @@ int32_t exec_gemm(skl_ctx *ctx, GemmLaunch g, const GemmPlan &p, char *ws, bool 
             g.mv = g.M;
             g.nv = g.N;
         }
-        SKL_TRY(timed_gemm(ctx, g, true));
+        SKL_TRY(timed_gemm(ctx, g, GemmKind::Dma));
     } else {
         if (p.splits > 1) {
             g.op = Op::DwPartial;
@@ -269,7 +303,7 @@ int32_t exec_gemm(skl_ctx *ctx, GemmLaunch g, const GemmPlan &p, char *ws, bool 
             g.st.split_stride = (uint64_t)M * N;
             g.st.ldc = N;
         }
-        SKL_TRY(timed_gemm(ctx, g, false));
+        SKL_TRY(timed_gemm(ctx, g, GemmKind::Staged));
     }
     if (p.splits > 1) {
         DwReduceArgs d{};
@@ -779,6 +813,7 @@ static int32_t backward_impl(skl_ctx *ctx, const skl_dense_desc *b, const void *
     g.b_kcontig = false;
     g.A = in;
     g.B = f16 ? b->d_prenorm_h : b->d_prenorm;
+    g.b32 = b->d_prenorm;
     g.splits = 1;
     g.op = Op::DwOpt;
     g.opt = oe;

@@ -402,6 +402,190 @@ uint32_t gemm_dma_splits(uint32_t K, uint32_t splits) {
     return (K + kps - 1) / kps;
 }
 
+// ---- skinny outputs (N <= 16) ---------------------------------------------------------
+// The output layers of the MLP configurations have 10 and 13 columns: a 256x256
+// (or 128x128) MFMA tile would be >90% padding, and the work is a stream over X.
+constexpr uint32_t SKINNY_N = 16;
+constexpr uint32_t SKINNY_LDS = 96 * 1024;
+
+// Sum of v[0..15] over the wave by recursive halving: each xor-shuffle step sends
+// half of the values a lane still holds and keeps the other half, so lane l ends
+// with column (l >> 2) & 15 summed over its 4 lanes after 8+4+2+1 shuffles, then 2
+// more finish it (17 in all, fixed order).  Returns the column sum lane l holds.
+__device__ __forceinline__ float wave_sum16(float (&v)[SKINNY_N], uint32_t lane) {
+#pragma unroll
+    for (int h = 8, m = 32; h >= 1; h >>= 1, m >>= 1) {
+        const bool up = (lane & (uint32_t)m) != 0;
+#pragma unroll
+        for (int i = 0; i < h; ++i) {
+            const float send = up ? v[i] : v[i + h];
+            const float keep = up ? v[i + h] : v[i];
+            v[i] = keep + __shfl_xor(send, m, 64);
+        }
+    }
+    float t = v[0];
+    t += __shfl_xor(t, 2, 64);
+    t += __shfl_xor(t, 1, 64);
+    return t;
+}
+
+// Forward, one wave per row: lane l takes the 8-element k chunks l, l + 64, ... of
+// the row (one 16-byte load per chunk on 16-byte aligned rows, 8 element loads
+// otherwise: a wave still covers 512 consecutive elements), and for each of the 16
+// columns one 16-byte LDS read of W^T (staged n-major, rows of Kp = K rounded up to
+// 8, zero past K and past N) feeds 8 FMAs into the lane's partial column sums.  The
+// sums are reduced over the wave, and the lane holding column n < N runs the forward
+// epilogue for it (bias, act, dropout, the three cache stores).  One workgroup per CU
+// stages W once for all of its rows.
+template <typename T, bool VECX>
+__global__ void __launch_bounds__(1024) skinny_fwd_kernel(GemmShape sh, const T *__restrict__ A,
+                                                          const T *__restrict__ B, FwdEpi ep) {
+    constexpr int CH = 8;   // k per chunk
+    __shared__ __attribute__((aligned(16))) T ws[SKINNY_LDS / sizeof(T)];
+    const uint32_t K = sh.K, N = sh.N, Kp = (K + CH - 1) / CH * CH;
+    for (uint32_t i = threadIdx.x; i < SKINNY_N * Kp; i += blockDim.x) {
+        const uint32_t n = i / Kp, k = i - n * Kp;
+        ws[i] = (n < N && k < K) ? B[(uint64_t)k * sh.ldb + n] : (T)0;
+    }
+    __syncthreads();
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    for (uint32_t m = blockIdx.x * waves + wave; m < sh.M; m += gridDim.x * waves) {
+        float acc[SKINNY_N];
+#pragma unroll
+        for (int n = 0; n < (int)SKINNY_N; ++n) acc[n] = 0.0f;
+        const T *x = A + (uint64_t)m * sh.lda;
+#pragma unroll 2
+        for (uint32_t k0 = lane * CH; k0 < K; k0 += 64 * CH) {
+            T xv[CH];
+            if (VECX && k0 + CH <= K) {
+                static_assert(sizeof(xv) % 16 == 0, "chunk of whole 16-byte words");
+#pragma unroll
+                for (int q = 0; q < (int)(sizeof(xv) / 16); ++q)
+                    reinterpret_cast<u32x4 *>(xv)[q] = reinterpret_cast<const u32x4 *>(x + k0)[q];
+            } else {
+#pragma unroll
+                for (int e = 0; e < CH; ++e) xv[e] = k0 + e < K ? x[k0 + e] : (T)0;
+            }
+#pragma unroll
+            for (int n = 0; n < (int)SKINNY_N; ++n) {
+                T w8[CH];
+#pragma unroll
+                for (int q = 0; q < (int)(sizeof(w8) / 16); ++q)
+                    reinterpret_cast<u32x4 *>(w8)[q] = reinterpret_cast<const u32x4 *>(ws + n * Kp + k0)[q];
+#pragma unroll
+                for (int e = 0; e < CH; ++e) acc[n] = fmaf(to_f32(xv[e]), to_f32(w8[e]), acc[n]);
+            }
+        }
+        const float z = wave_sum16(acc, lane);
+        const uint32_t n = (lane >> 2) & 15u;
+        if ((lane & 3u) == 0 && n < N) {
+            GemmShape one = sh;   // column n alone
+            one.N = n + 1;
+            EpiFwdK<T>::apply(ep, one, m, n, floatx4{z, 0.0f, 0.0f, 0.0f}, 0);
+        }
+    }
+}
+
+bool skinny_fwd_ok(const GemmLaunch &g) {
+    const size_t esz = g.dtype == 1 ? 2 : 4;
+    const size_t kp = (g.K + 7) / 8 * 8;
+    return g.op == Op::Fwd && g.N <= SKINNY_N && g.a_kcontig && !g.b_kcontig && g.K > 0 &&
+           (size_t)SKINNY_N * kp * esz <= SKINNY_LDS;
+}
+
+template <typename T> static void launch_skinny_fwd_t(const GemmShape &sh, const GemmLaunch &g, hipStream_t s) {
+    const bool vecx = sh.lda % 8 == 0 && (reinterpret_cast<uintptr_t>(g.A) & 15u) == 0;
+    uint32_t grid = (sh.M + 15) / 16;   // 16 waves per workgroup, a row per wave at a time
+    if (grid > 256) grid = 256;
+    const T *A = reinterpret_cast<const T *>(g.A), *B = reinterpret_cast<const T *>(g.B);
+    if (vecx)
+        hipLaunchKernelGGL((skinny_fwd_kernel<T, true>), dim3(grid), dim3(1024), 0, s, sh, A, B, g.fwd);
+    else
+        hipLaunchKernelGGL((skinny_fwd_kernel<T, false>), dim3(grid), dim3(1024), 0, s, sh, A, B, g.fwd);
+}
+
+hipError_t launch_skinny_fwd(const GemmLaunch &g, hipStream_t s) {
+    if (!skinny_fwd_ok(g)) return hipErrorInvalidValue;
+    GemmShape sh{};
+    sh.M = g.M;
+    sh.N = g.N;
+    sh.K = g.K;
+    sh.lda = g.lda;
+    sh.ldb = g.ldb;
+    if (g.dtype == 1)
+        launch_skinny_fwd_t<half_t>(sh, g, s);
+    else
+        launch_skinny_fwd_t<float>(sh, g, s);
+    return hipGetLastError();
+}
+
+// dW partial sums, thread per W row: thread k of workgroup (x, y) walks the batch rows
+// of slice y in order, acc[n] += X[b][k] * dP[b][n], with 64 rows of dP (fp32) at a
+// time in LDS (broadcast reads); partials[y][k][0..15].
+template <typename T> __global__ void __launch_bounds__(256) skinny_dw_kernel(GemmShape sh, const T *__restrict__ X,
+                                                                             const float *__restrict__ dp,
+                                                                             float *__restrict__ partials,
+                                                                             uint32_t per) {
+    __shared__ float dps[64][SKINNY_N];
+    const uint32_t K = sh.M, N = sh.N;          // output [K x N]; reduction over sh.K batch rows
+    const uint32_t k = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t r0 = blockIdx.y * per;
+    const uint32_t r1 = min(sh.K, r0 + per);
+    float acc[SKINNY_N];
+#pragma unroll
+    for (int n = 0; n < (int)SKINNY_N; ++n) acc[n] = 0.0f;
+    for (uint32_t rb = r0; rb < r1; rb += 64) {
+        const uint32_t nrows = min(64u, r1 - rb);
+        __syncthreads();
+        for (uint32_t i = threadIdx.x; i < 64 * SKINNY_N; i += 256) {
+            const uint32_t r = i / SKINNY_N, n = i % SKINNY_N;
+            dps[r][n] = (r < nrows && n < N) ? dp[(uint64_t)(rb + r) * sh.ldb + n] : 0.0f;
+        }
+        __syncthreads();
+        if (k < K) {
+#pragma unroll 4
+            for (uint32_t r = 0; r < nrows; ++r) {
+                const float xv = to_f32(X[(uint64_t)(rb + r) * sh.lda + k]);
+#pragma unroll
+                for (int n = 0; n < (int)SKINNY_N; ++n) acc[n] = fmaf(xv, dps[r][n], acc[n]);
+            }
+        }
+    }
+    if (k >= K) return;
+    float *p = partials + ((uint64_t)blockIdx.y * K + k) * SKINNY_N;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<floatx4 *>(p + 4 * q) = floatx4{acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]};
+}
+
+uint32_t skinny_dw_slices(uint32_t rows, uint32_t K) {
+    const uint32_t col_blocks = (K + 255) / 256;
+    uint32_t sl = (1024 + col_blocks - 1) / col_blocks;
+    const uint32_t cap = (rows + 63) / 64;
+    if (sl > cap) sl = cap;
+    return sl < 1 ? 1 : sl;
+}
+
+hipError_t launch_skinny_dw(const GemmLaunch &g, float *partials, uint32_t slices, hipStream_t s) {
+    if (g.N > SKINNY_N || g.a_kcontig || !g.b32 || (reinterpret_cast<uintptr_t>(partials) & 15u))
+        return hipErrorInvalidValue;
+    GemmShape sh{};
+    sh.M = g.M;          // W rows (inputs)
+    sh.N = g.N;          // W cols (outputs)
+    sh.K = g.K;          // batch rows
+    sh.lda = g.lda;      // X row pitch
+    sh.ldb = g.N;        // d_prenorm row pitch
+    const uint32_t per = (g.K + slices - 1) / slices;
+    const dim3 grid((g.M + 255) / 256, slices);
+    if (g.dtype == 1)
+        hipLaunchKernelGGL(skinny_dw_kernel<half_t>, grid, dim3(256), 0, s, sh,
+                           reinterpret_cast<const half_t *>(g.A), g.b32, partials, per);
+    else
+        hipLaunchKernelGGL(skinny_dw_kernel<float>, grid, dim3(256), 0, s, sh,
+                           reinterpret_cast<const float *>(g.A), g.b32, partials, per);
+    return hipGetLastError();
+}
+
 hipError_t launch_gemm(const GemmLaunch &g, hipStream_t s) {
     if (g.M == 0 || g.N == 0) return hipSuccess;
     if (gemm_direct_ok(g)) return launch_gemm_dma(g, s);

@@ -54,9 +54,17 @@ struct GemmLaunch {
     FwdEpi fwd;
     OptEpi opt;
     StoreEpi st;
+    const float *b32;     // dW: fp32 d_prenorm (ld N), read by the skinny kernel instead of B
 };
 
 hipError_t launch_gemm(const GemmLaunch &g, hipStream_t stream);
+// Skinny outputs (N <= 16).  Forward: a streaming kernel, W staged in LDS
+// (fits when skinny_fwd_ok).  dW: batch-sliced partial sums of X^T . d_prenorm
+// (fp32) into partials [slices x K x 16]; skinny_dw_slices gives the slice count.
+bool skinny_fwd_ok(const GemmLaunch &g);
+hipError_t launch_skinny_fwd(const GemmLaunch &g, hipStream_t stream);
+uint32_t skinny_dw_slices(uint32_t rows, uint32_t K);
+hipError_t launch_skinny_dw(const GemmLaunch &g, float *partials, uint32_t slices, hipStream_t stream);
 // The 256x256 direct-to-LDS kernel on operands that fit it (gemm_dma_shape_ok):
 // M, N whole 256 tiles (zero-padded copies allowed: the epilogue stops at mv, nv),
 // K a multiple of 128; DwPartial may split K into g.splits slices.

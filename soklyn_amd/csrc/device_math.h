@@ -31,6 +31,16 @@ template <typename T> __device__ __forceinline__ f32x4 load4(const void *p, uint
         return *reinterpret_cast<const f32x4 *>(reinterpret_cast<const float *>(p) + i);
     }
 }
+// store4 with the nontemporal hint: outputs written once and read by a later
+// kernel, kept from displacing the GEMM's operand panels in L2.
+template <typename T> __device__ __forceinline__ void store4_nt(void *p, uint64_t i, f32x4 v) {
+    if constexpr (sizeof(T) == 2) {
+        __builtin_nontemporal_store(f16x4{(half_t)v.x, (half_t)v.y, (half_t)v.z, (half_t)v.w},
+                                    reinterpret_cast<f16x4 *>(reinterpret_cast<half_t *>(p) + i));
+    } else {
+        __builtin_nontemporal_store(v, reinterpret_cast<f32x4 *>(reinterpret_cast<float *>(p) + i));
+    }
+}
 template <typename T> __device__ __forceinline__ void store4(void *p, uint64_t i, f32x4 v) {
     if constexpr (sizeof(T) == 2) {
         *reinterpret_cast<f16x4 *>(reinterpret_cast<half_t *>(p) + i) =

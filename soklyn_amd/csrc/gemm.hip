@@ -40,13 +40,13 @@ template <typename T> struct EpiFwdK {
         // 4 consecutive columns: one 8-byte (fp16) / 16-byte (fp32) access per tensor
         f32x4 z = v;
         if (e.bias) z = z + col.bias;
-        store4<T>(e.z_out, idx, z);
+        store4_nt<T>(e.z_out, idx, z);
         if (!e.fuse_act) return;
         const f32x4 zt = round4<T>(z);
         f32x4 a;
 #pragma unroll
         for (int j = 0; j < 4; ++j) a[j] = activation(e.act, zt[j], e.leaky);
-        store4<T>(e.predrop, idx, a);
+        store4_nt<T>(e.predrop, idx, a);
         if (e.use_dropout) {
             const float scale = 1.0f / (1.0f - e.p);
             f32x4 mk, o;
@@ -56,10 +56,10 @@ template <typename T> struct EpiFwdK {
                 mk[j] = keep ? scale : 0.0f;
                 o[j] = keep ? a[j] * scale : 0.0f;
             }
-            store4<T>(e.mask, idx, mk);
-            store4<T>(e.out, idx, o);
+            store4_nt<T>(e.mask, idx, mk);
+            store4_nt<T>(e.out, idx, o);
         } else {
-            store4<T>(e.out, idx, a);
+            store4_nt<T>(e.out, idx, a);
         }
     }
     __device__ __forceinline__ static void apply(const FwdEpi &e, const GemmShape &sh, uint32_t m, uint32_t n,
@@ -114,7 +114,7 @@ struct EpiStoreK {
     __device__ __forceinline__ static void load(const StoreEpi &, uint64_t, uint32_t, Pre &) {}
     __device__ __forceinline__ static void finish(const StoreEpi &e, uint64_t idx, uint32_t, uint32_t, floatx4 v,
                                                   const Col &, const Pre &) {
-        *reinterpret_cast<floatx4 *>(e.out + idx) = v;
+        __builtin_nontemporal_store(v, reinterpret_cast<floatx4 *>(e.out + idx));
     }
     __device__ __forceinline__ static void apply(const StoreEpi &e, const GemmShape &sh, uint32_t m, uint32_t n,
                                                  floatx4 v, uint32_t split) {

@@ -14,17 +14,21 @@
 //    layout 1-3% slower, so the launcher picks per layout.
 //  * BK = 64 halves; 2 stages of 64 KB (A tile + B tile, 32 KB each, laid out
 //    per operand layout as described at OpK / OpN).  Stages are filled by
-//    global_load_lds_dwordx4 (no staging registers, no ds_write): one wave
+//    buffer_load_dwordx4 ... lds (no staging registers, no ds_write): one wave
 //    instruction fills 1 KB of LDS, each lane fetching the global chunk that
 //    the swizzle puts in its slot; a wave issues 32 / NW per operand per tile.
+//    The buffer form (32-bit lane offset + scalar offset against a resource)
+//    ran 1-3% faster than global_load_lds_dwordx4 (64-bit lane addresses) on
+//    the C3 shapes.
 //  * Fragments are software-pipelined across the per-tile barrier: the four
 //    k-steps of a tile alternate between two fragment register sets, and the
 //    MFMAs of a tile's last k-step are issued after the barrier, behind the
 //    reads of the next tile's first k-step.
 //  * Per tile: wait for this wave's DMA of the next tile (vmcnt 0: it is the
 //    only one outstanding), s_barrier without a fence (LDS DMA completion is
-//    what vmcnt tracks), then DMA tile kt+2 into the stage every wave has just
-//    finished reading.
+//    what vmcnt tracks), then the reads of the next tile's first k-step, and
+//    the last k-step's MFMAs with one DMA instruction of tile kt+2 (into the
+//    stage every wave has just finished reading) behind each MFMA.
 //  * The k loop body has no branches (a branchy body made the register
 //    allocator spill): K is a multiple of 2 k-tiles, the last two
 //    refills fetch the final k-tile again (in bounds, never read), and the last
@@ -56,10 +60,22 @@ template <int NW_> struct DmaCfg {
 typedef __attribute__((address_space(3))) char lds_char;
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-__device__ __forceinline__ void dma16(const char *src, lds_char *dst) {
-    __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(src),
-                                     reinterpret_cast<__attribute__((address_space(3))) void *>(dst), 16, 0, 0);
-}
+// Direct-to-LDS source of one lane: a raw buffer resource over the operand
+// (gfx9 dword 3 = 0x00020000) and the lane's byte offset.  load() moves the
+// lane's 16 bytes at voff + add to dst + 16 lane (buffer_load_dwordx4 ... lds;
+// the immediate offset, which would move the LDS address too, stays 0).
+struct DmaSrc {
+    __amdgpu_buffer_rsrc_t rsrc;
+    uint32_t voff;
+    __device__ __forceinline__ void init(const half_t *p, uint32_t bytes, uint32_t off) {
+        rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t *>(p), (short)0, (int)bytes, 0x00020000);
+        voff = off;
+    }
+    __device__ __forceinline__ void load(uint32_t add, lds_char *dst) const {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, reinterpret_cast<__attribute__((address_space(3))) void *>(dst),
+                                                 16, (int)voff, (int)add, 0, 0);
+    }
+};
 
 // s_waitcnt with only one counter constrained (gfx9 encoding: vmcnt[3:0] +
 // vmcnt[5:4] at bits 15:14, expcnt bits 6:4, lgkmcnt bits 11:8).
@@ -84,7 +100,7 @@ __device__ __forceinline__ void pin(u32x2 &v) { asm volatile("" : "+v"(v)); }
 
 // ---- operand staging ------------------------------------------------------------
 // One operand tile of a stage: 256 rows (m or n) x 64 k, 32 KB, filled by
-// global_load_lds_dwordx4 (one wave instruction = 1 KB of LDS, lane l writing
+// direct-to-LDS loads (one wave instruction = 1 KB of LDS, lane l writing
 // bytes 16 l .. 16 l + 15; instruction t of wave w fills KB NW t + w), read
 // as NF 32-row MFMA fragments of the wave's rows per k-step.  The fragment of
 // a lane holds 8 consecutive k of row l % 32 (k = 8 (l / 32) .. + 7 within
@@ -98,27 +114,25 @@ template <int NW, int NF> struct OpK {
     static constexpr int READS = NF;   // ds_read per k-step
     static constexpr int IPO = 32 / NW;   // DMA instructions per tile and wave
     struct Frag { u32x4 v[NF]; };
-    const char *src;                  // DMA source of this lane, t = 0, k-tile 0
+    DmaSrc dma;                       // DMA source of this lane, t = 0, k-tile 0
     uint32_t step;                    // bytes between DMA instructions (8 NW rows)
     uint32_t lds;                     // LDS byte address of this lane's fragment row, stage 0
     uint32_t g;                       // swizzle term of the fragment row
 
-    __device__ __forceinline__ void init(const half_t *p, uint32_t ld, uint32_t mn0, uint32_t wbase,
+    __device__ __forceinline__ void init(const half_t *p, uint32_t ld, uint32_t rows, uint32_t mn0, uint32_t wbase,
                                          uint32_t wave, uint32_t lane, uint32_t lds_op) {
         // instruction t fills rows 8 (NW t + wave) .. + 7; lane -> row + lane / 8, slot lane % 8;
         // (row >> 1) & 7 does not depend on t (8 NW t >> 1 is a multiple of 8)
         const uint32_t row0 = 8u * wave + (lane >> 3);
         const uint32_t kc = (lane & 7u) ^ ((row0 >> 1) & 7u);
-        src = reinterpret_cast<const char *>(p) + ((size_t)(mn0 + row0) * ld * 2u + kc * 16u);
+        dma.init(p, rows * ld * 2u, (mn0 + row0) * ld * 2u + kc * 16u);
         step = 8u * NW * ld * 2u;
         const uint32_t frow = lane & 31u;
         g = (lane >> 5) ^ ((frow >> 1) & 7u);
         lds = lds_op + (wbase + frow) * 128u;
     }
-    __device__ __forceinline__ void issue(int kt, lds_char *dst) const {
-        const char *s = src + (uint32_t)kt * 128u;
-#pragma unroll
-        for (int t = 0; t < IPO; ++t) dma16(s + t * step, dst + t * (NW * 1024u));
+    __device__ __forceinline__ void issue(int kt, int t, lds_char *dst) const {
+        dma.load((uint32_t)kt * 128u + t * step, dst + t * (NW * 1024u));
     }
     // logical chunk 2 ks + (lane / 32) of each fragment row; fragment i is 32 rows further on
     __device__ __forceinline__ void read(Frag &f, uint32_t stage_off, int ks) const {
@@ -151,18 +165,18 @@ template <int NW, int NF> struct OpN {
     static constexpr int READS = 2 * NF;
     static constexpr int IPO = 32 / NW;
     struct Frag { u32x2 v[NF][2]; };
-    const char *src;
+    DmaSrc dma;
     uint32_t step;                    // 2 NW k-rows per DMA instruction of a wave
     uint32_t kstep;                   // bytes per k-tile (64 k-rows)
     uint32_t lds[NF];                 // per fragment i, stage 0, k-step 0, h = 0
 
-    __device__ __forceinline__ void init(const half_t *p, uint32_t ld, uint32_t mn0, uint32_t wbase,
+    __device__ __forceinline__ void init(const half_t *p, uint32_t ld, uint32_t rows, uint32_t mn0, uint32_t wbase,
                                          uint32_t wave, uint32_t lane, uint32_t lds_op) {
         // instruction t (q = wave + NW t) fills k-rows 2 q, 2 q + 1; lane -> k-row 2 q + lane / 32,
         // slot lane % 32; the swizzle term (k-row & 3) does not depend on t (NW is even)
         const uint32_t r0 = 2u * wave + (lane >> 5);
         const uint32_t cl = (lane & 31u) ^ (4u * (r0 & 3u));
-        src = reinterpret_cast<const char *>(p) + ((size_t)r0 * ld * 2u + mn0 * 2u + cl * 16u);
+        dma.init(p, rows * ld * 2u, r0 * ld * 2u + mn0 * 2u + cl * 16u);
         step = 2u * NW * ld * 2u;
         kstep = 64u * ld * 2u;
         const uint32_t grp = lane >> 4, s = lane & 15u;
@@ -172,10 +186,8 @@ template <int NW, int NF> struct OpN {
 #pragma unroll
         for (int i = 0; i < NF; ++i) lds[i] = lds_op + (rel ^ (64u * i));
     }
-    __device__ __forceinline__ void issue(int kt, lds_char *dst) const {
-        const char *s = src + (uint32_t)kt * kstep;
-#pragma unroll
-        for (int t = 0; t < IPO; ++t) dma16(s + t * step, dst + t * (NW * 1024u));
+    __device__ __forceinline__ void issue(int kt, int t, lds_char *dst) const {
+        dma.load((uint32_t)kt * kstep + t * step, dst + t * (NW * 1024u));
     }
     // k-rows 16 ks + 4 h (+ 8): offsets 8192 ks + 2048 h keep the swizzle (multiples of 4 rows)
     __device__ __forceinline__ void read(Frag &f, uint32_t stage_off, int ks) const {
@@ -241,13 +253,15 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
     const uint32_t lds0 = (uint32_t)(uintptr_t)lsm;   // LDS byte address of smem
     OA oa;
     OB ob;
-    oa.init(A, sh.lda, m0, wm * C::TWM, wave, lane, lds0);
-    ob.init(B, sh.ldb, n0, wn * C::TWN, wave, lane, lds0 + C::OPB);
+    oa.init(A, sh.lda, A_KC ? sh.M : sh.K, m0, wm * C::TWM, wave, lane, lds0);
+    ob.init(B, sh.ldb, B_KC ? sh.N : sh.K, n0, wn * C::TWN, wave, lane, lds0 + C::OPB);
 
     auto issue = [&](int kt, int stage) {
         lds_char *st = lsm + stage * C::STAGEB + wave * 1024u;
-        oa.issue(kt, st);
-        ob.issue(kt, st + C::OPB);
+#pragma unroll
+        for (int t = 0; t < OA::IPO; ++t) oa.issue(kt, t, st);
+#pragma unroll
+        for (int t = 0; t < OB::IPO; ++t) ob.issue(kt, t, st + C::OPB);
     };
 
     floatx16 acc[C::MT][C::NTL];
@@ -292,13 +306,23 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
             mma(1);
             read(1, s, 3);
             mma(0);
-            // k-step 3: cross the barrier before issuing its MFMAs
+            // k-step 3: cross the barrier before issuing its MFMAs (k-step 2's
+            // stay above it: the scheduling region ends here)
+            __builtin_amdgcn_sched_barrier(0);
             wait_lgkmcnt<0>();                  // set 1 (k-step 3) is in registers
             wait_vmcnt<0>();                    // this wave's DMA of tile kt+1 landed
             __builtin_amdgcn_s_barrier();       // everyone's landed; stage s fully read
-            issue(min(kb + kt + 2, klast), s);
             read(0, s ^ 1, 0);
             mma(1);
+            issue(min(kb + kt + 2, klast), s);
+            // one DMA instruction behind each MFMA of k-step 3 (0x008: MFMA,
+            // 0x020: VMEM read); the scheduling region ends here
+#pragma unroll
+            for (int q = 0; q < C::MT * C::NTL; ++q) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                if (q < OA::IPO + OB::IPO) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
     wait_vmcnt<0>();     // no DMA may land in the epilogue's staging area

@@ -20,15 +20,19 @@
 //    The buffer form (32-bit lane offset + scalar offset against a resource)
 //    ran 1-3% faster than global_load_lds_dwordx4 (64-bit lane addresses) on
 //    the C3 shapes.
-//  * Fragments are software-pipelined across the per-tile barrier: the four
-//    k-steps of a tile alternate between two fragment register sets, and the
-//    MFMAs of a tile's last k-step are issued after the barrier, behind the
-//    reads of the next tile's first k-step.
-//  * Per tile: wait for this wave's DMA of the next tile (vmcnt 0: it is the
-//    only one outstanding), s_barrier without a fence (LDS DMA completion is
-//    what vmcnt tracks), then the reads of the next tile's first k-step, and
-//    the last k-step's MFMAs with one DMA instruction of tile kt+2 (into the
-//    stage every wave has just finished reading) behind each MFMA.
+//  * Fragments are software-pipelined: the four k-steps of a tile alternate
+//    between two fragment register sets, and the reads of k-step ks + 1 are
+//    issued between the MFMAs of k-step ks, one fragment (two at 8 waves)
+//    behind each MFMA from the first on, so no burst of reads fills the LDS
+//    queues and the rest of the k-step covers their latency (scheduling
+//    barriers hold that order; 1-2% faster than the whole next set read ahead
+//    of the MFMAs).
+//  * Per tile: after k-step 2's MFMAs, wait for this wave's DMA of the next
+//    tile (vmcnt 0: it is the only one outstanding) and for k-step 3's
+//    fragments, s_barrier without a fence (LDS DMA completion is what vmcnt
+//    tracks); then k-step 3's MFMAs, each followed by one DMA instruction of
+//    tile kt+2 (into the stage every wave has just finished reading) and the
+//    reads of the next tile's k-step 0.
 //  * The k loop body has no branches (a branchy body made the register
 //    allocator spill): K is a multiple of 2 k-tiles, the last two
 //    refills fetch the final k-tile again (in bounds, never read), and the last
@@ -36,11 +40,11 @@
 //  * Fragment reads are inline ds_read_b128 / ds_read_b64_tr_b16 (left to
 //    itself the compiler sinks each read next to its first MFMA behind an
 //    lgkmcnt(0), serialising LDS latency with the MFMA pipe).  The compiler
-//    does not count them, so the kernel waits for them itself: before a
-//    fragment set is consumed at most the other set's reads may be pending
-//    (LDS returns in order; a scalar load in flight only makes the wait
-//    stricter), and after the wait an empty asm statement per fragment
-//    register claims to rewrite it, so no MFMA can be scheduled above the wait.
+//    does not count them, so the kernel waits for them itself: when a set is
+//    about to be consumed its reads are the only ones pending, so the wait is
+//    lgkmcnt(0) (a scalar load in flight only makes it stricter), and after
+//    it an empty asm statement per fragment register claims to rewrite it, so
+//    no MFMA can be scheduled above the wait.
 // Operand offsets are 32-bit (rows * ld * 2 bytes < 4 GiB).
 #pragma once
 
@@ -111,7 +115,6 @@ __device__ __forceinline__ void pin(u32x2 &v) { asm volatile("" : "+v"(v)); }
 // 16 consecutive rows of one chunk column hit 16 distinct 16-byte bank groups.
 // A fragment is one ds_read_b128.
 template <int NW, int NF> struct OpK {
-    static constexpr int READS = NF;   // ds_read per k-step
     static constexpr int IPO = 32 / NW;   // DMA instructions per tile and wave
     struct Frag { u32x4 v[NF]; };
     DmaSrc dma;                       // DMA source of this lane, t = 0, k-tile 0
@@ -134,14 +137,14 @@ template <int NW, int NF> struct OpK {
     __device__ __forceinline__ void issue(int kt, int t, lds_char *dst) const {
         dma.load((uint32_t)kt * 128u + t * step, dst + t * (NW * 1024u));
     }
-    // logical chunk 2 ks + (lane / 32) of each fragment row; fragment i is 32 rows further on
-    __device__ __forceinline__ void read(Frag &f, uint32_t stage_off, int ks) const {
+    // fragment i: logical chunk 2 ks + (lane / 32) of row 32 i + lane % 32
+    __device__ __forceinline__ void read_frag(Frag &f, uint32_t stage_off, int ks, int i) const {
         const uint32_t a = lds + stage_off + ((2u * ks) ^ g) * 16u;
-        ds_read16<0 * 4096>(f.v[0], a);
-        ds_read16<1 * 4096>(f.v[1], a);
-        if constexpr (NF > 2) {
-            ds_read16<2 * 4096>(f.v[2], a);
-            ds_read16<3 * 4096>(f.v[3], a);
+        switch (i) {
+        case 0: ds_read16<0>(f.v[0], a); break;
+        case 1: ds_read16<4096>(f.v[1], a); break;
+        case 2: if constexpr (NF > 2) ds_read16<8192>(f.v[2], a); break;
+        default: if constexpr (NF > 3) ds_read16<12288>(f.v[3], a); break;
         }
     }
     __device__ __forceinline__ static u32x4 op(const Frag &f, int i) { return f.v[i]; }
@@ -162,7 +165,6 @@ template <int NW, int NF> struct OpK {
 // further on: chunk + 4 i, i.e. the lane's address XOR 64 i (the wave's first
 // row is a multiple of 32 NF, so the chunk bits that i flips start clear).
 template <int NW, int NF> struct OpN {
-    static constexpr int READS = 2 * NF;
     static constexpr int IPO = 32 / NW;
     struct Frag { u32x2 v[NF][2]; };
     DmaSrc dma;
@@ -190,12 +192,9 @@ template <int NW, int NF> struct OpN {
         dma.load((uint32_t)kt * kstep + t * step, dst + t * (NW * 1024u));
     }
     // k-rows 16 ks + 4 h (+ 8): offsets 8192 ks + 2048 h keep the swizzle (multiples of 4 rows)
-    __device__ __forceinline__ void read(Frag &f, uint32_t stage_off, int ks) const {
-#pragma unroll
-        for (int i = 0; i < NF; ++i) {
-            ds_read8_tr<0>(f.v[i][0], lds[i] + stage_off + 8192u * ks);
-            ds_read8_tr<2048>(f.v[i][1], lds[i] + stage_off + 8192u * ks);
-        }
+    __device__ __forceinline__ void read_frag(Frag &f, uint32_t stage_off, int ks, int i) const {
+        ds_read8_tr<0>(f.v[i][0], lds[i] + stage_off + 8192u * ks);
+        ds_read8_tr<2048>(f.v[i][1], lds[i] + stage_off + 8192u * ks);
     }
     __device__ __forceinline__ static u32x4 op(const Frag &f, int i) {
         return u32x4{f.v[i][0].x, f.v[i][0].y, f.v[i][1].x, f.v[i][1].y};
@@ -224,9 +223,6 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
     typedef DmaCfg<NW> C;
     typedef typename DmaOpSel<A_KC, NW, C::MT>::type OA;
     typedef typename DmaOpSel<B_KC, NW, C::NTL>::type OB;
-    // a fragment set may be consumed while at most the other set's reads are pending
-    constexpr int SET_READS = OA::READS + OB::READS;
-    constexpr int WAIT_SET = SET_READS < 15 ? SET_READS : 15;
     constexpr int EPITCH = C::BN + 4;
     constexpr int MTP = 2;                                   // accumulator rows per epilogue pass
     constexpr int PROWS = C::WM * MTP * 32;
@@ -274,18 +270,54 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
 
     typename OA::Frag fa[2];
     typename OB::Frag fb[2];
-    auto read = [&](int set, int stage, int ks) {
-        oa.read(fa[set], stage * C::STAGEB, ks);
-        ob.read(fb[set], stage * C::STAGEB, ks);
+    constexpr int NFR = C::MT + C::NTL;            // fragments per set
+    constexpr int NMM = C::MT * C::NTL;            // MFMAs per k-step
+    constexpr int NDMA = OA::IPO + OB::IPO;        // DMA instructions per tile and wave
+    constexpr int FPM = NW == 8 ? 2 : 1;           // fragment reads behind each MFMA
+    static_assert(NFR <= NMM * FPM && NDMA <= NMM, "every read and DMA has an MFMA to follow");
+    auto read_frag = [&](int set, int stage, int ks, int f) {
+        if (f < C::MT)
+            oa.read_frag(fa[set], stage * C::STAGEB, ks, f);
+        else
+            ob.read_frag(fb[set], stage * C::STAGEB, ks, f - C::MT);
     };
-    auto mma = [&](int set) {
-        asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(WAIT_SET));
-        OA::pin_all(fa[set]);
-        OB::pin_all(fb[set]);
+    auto read = [&](int set, int stage, int ks) {
 #pragma unroll
-        for (int i = 0; i < C::MT; ++i)
+        for (int f = 0; f < NFR; ++f) read_frag(set, stage, ks, f);
+    };
+    auto mfma = [&](int set, int q) {
+        const int i = q / C::NTL, j = q % C::NTL;
+        Mfma<half_t>::run(acc[i][j], OB::op(fb[set], j), OA::op(fa[set], i));
+    };
+    auto dma = [&](int kt, int stage, int q) {
+        lds_char *st = lsm + stage * C::STAGEB + wave * 1024u;
+        if (q < OA::IPO)
+            oa.issue(kt, q, st);
+        else
+            ob.issue(kt, q - OA::IPO, st + C::OPB);
+    };
+    // The fragment set `cur` is complete (its reads were the only LDS reads
+    // pending), and no MFMA on it may be scheduled above this point.
+    auto land = [&](int cur) {
+        wait_lgkmcnt<0>();
+        OA::pin_all(fa[cur]);
+        OB::pin_all(fb[cur]);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // One k-step: MFMA q of set `cur`, then FPM fragment reads of the next
+    // k-step into the other set (all of them within the first NFR / FPM MFMAs,
+    // so the rest of the k-step covers their latency), with scheduling barriers
+    // keeping that order.
+    auto kstep = [&](int cur, int stage, int ks_next) {
+        land(cur);
 #pragma unroll
-            for (int j = 0; j < C::NTL; ++j) Mfma<half_t>::run(acc[i][j], OB::op(fb[set], j), OA::op(fa[set], i));
+        for (int q = 0; q < NMM; ++q) {
+            mfma(cur, q);
+#pragma unroll
+            for (int u = 0; u < FPM; ++u)
+                if (q * FPM + u < NFR) read_frag(cur ^ 1, stage, ks_next, q * FPM + u);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     };
 
     // prologue: tile 0 resident, tile 1 in flight, first fragments read
@@ -300,29 +332,26 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
             const int kt = kt0 + s;
-            read(1, s, 1);
-            mma(0);
-            read(0, s, 2);
-            mma(1);
-            read(1, s, 3);
-            mma(0);
-            // k-step 3: cross the barrier before issuing its MFMAs (k-step 2's
-            // stay above it: the scheduling region ends here)
-            __builtin_amdgcn_sched_barrier(0);
-            wait_lgkmcnt<0>();                  // set 1 (k-step 3) is in registers
+            kstep(0, s, 1);
+            kstep(1, s, 2);
+            kstep(0, s, 3);
+            // k-step 3 crosses the barrier: after it, MFMA q of set 1 is followed
+            // by DMA instruction q of tile kt+2 (into the stage every wave has
+            // just finished reading) and the reads of the next tile's k-step 0
             wait_vmcnt<0>();                    // this wave's DMA of tile kt+1 landed
-            __builtin_amdgcn_s_barrier();       // everyone's landed; stage s fully read
-            read(0, s ^ 1, 0);
-            mma(1);
-            issue(min(kb + kt + 2, klast), s);
-            // one DMA instruction behind each MFMA of k-step 3 (0x008: MFMA,
-            // 0x020: VMEM read); the scheduling region ends here
-#pragma unroll
-            for (int q = 0; q < C::MT * C::NTL; ++q) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                if (q < OA::IPO + OB::IPO) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-            }
+            land(1);                            // set 1 (k-step 3) is in registers
+            __builtin_amdgcn_s_barrier();       // everyone's DMA landed; stage s fully read
             __builtin_amdgcn_sched_barrier(0);
+            const int kn = min(kb + kt + 2, klast);
+#pragma unroll
+            for (int q = 0; q < NMM; ++q) {
+                mfma(1, q);
+                if (q < NDMA) dma(kn, s, q);
+#pragma unroll
+                for (int u = 0; u < FPM; ++u)
+                    if (q * FPM + u < NFR) read_frag(0, s ^ 1, 0, q * FPM + u);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
     }
     wait_vmcnt<0>();     // no DMA may land in the epilogue's staging area

@@ -343,13 +343,12 @@ bool gemm_direct_ok(const GemmLaunch &g) {
            (g.splits == 0 || g.splits == 1);
 }
 
-// Waves per workgroup: 8 when an operand is read through the transposing LDS
-// path (its 8-byte reads leave one wave per SIMD waiting on LDS latency), 4
-// when both operands are k-contiguous (see gemm_dma.h).
+// 8 waves per workgroup for every layout (two per SIMD: one issues MFMAs while
+// the other waits on LDS; see gemm_dma.h).
 template <class Epi, bool AK, bool BK_>
 static hipError_t run_dma(const GemmLaunch &g, const typename Epi::Params &p, uint32_t splits, uint32_t kps,
                           hipStream_t s) {
-    constexpr int NW = (AK && BK_) ? 4 : 8;
+    constexpr int NW = 8;
     GemmShape sh{};
     sh.M = g.M;
     sh.N = g.N;

@@ -9,9 +9,10 @@
 //    waves per SIMD, wave tile 128 x 64 (4 x 2 blocks, 128 accumulators), 1.5x
 //    the LDS fragment bytes per flop, but while one wave of a SIMD waits on its
 //    LDS reads the other issues MFMAs.  Measured on the C3 shapes (random fp16
-//    data, 20 launches back to back): 8 waves run the layouts with a
-//    transposing (m/n-contiguous) operand 6-7% faster, and the all-k-contiguous
-//    layout 1-3% slower, so the launcher picks per layout.
+//    data, 30 launches back to back): 8 waves run the layouts with a
+//    transposing (m/n-contiguous) operand 6-7% faster and, with the
+//    interleaved schedule below, the all-k-contiguous layout 2% faster, so the
+//    launcher uses 8.
 //  * BK = 64 halves; 2 stages of 64 KB (A tile + B tile, 32 KB each, laid out
 //    per operand layout as described at OpK / OpN).  Stages are filled by
 //    buffer_load_dwordx4 ... lds (no staging registers, no ds_write): one wave

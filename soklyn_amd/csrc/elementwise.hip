@@ -4,6 +4,9 @@
 // split-K dW reduction + optimiser.
 #include "launch.h"
 
+#include <type_traits>
+#include <utility>
+
 namespace skl {
 
 template <typename T> __device__ __forceinline__ T ldv(const void *p, uint64_t i) {
@@ -366,54 +369,184 @@ hipError_t launch_softmax(uint32_t dtype, void *out, uint32_t rows, uint32_t n, 
 }
 
 // ---- error kernels ------------------------------------------------------------------
-// A thread owns 4 consecutive elements of one row.  VEC (n % 4 == 0, 16-byte
-// aligned buffers): 16-byte fp32 / 8-byte fp16 accesses; otherwise element
-// accesses of the cnt <= 4 columns that exist.
-template <typename T, bool VEC> struct Grp {
-    __device__ __forceinline__ static f32x4 ld(const void *p, uint64_t i, uint32_t cnt) {
-        if constexpr (VEC) {
-            return load4<T>(p, i);
-        } else {
-            f32x4 v = {0, 0, 0, 0};
-#pragma unroll
-            for (uint32_t j = 0; j < 4; ++j)
-                if (j < cnt) v[j] = to_f32(ldv<T>(p, i + j));
-            return v;
-        }
+// A thread owns 4 consecutive elements of one row (cnt <= 4 of them exist).
+// VEC (n % 4 == 0, 16-byte aligned buffers): GrpV, 16-byte fp32 / 8-byte fp16
+// accesses; otherwise GrpUA below.
+template <typename T> struct GrpV {
+    __device__ __forceinline__ static f32x4 ld(const void *p, uint64_t i, uint32_t) { return load4<T>(p, i); }
+    __device__ __forceinline__ static f32x4 ldf(const float *p, uint64_t i, uint32_t, bool nt = false) {
+        return nt ? __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p + i))
+                  : *reinterpret_cast<const f32x4 *>(p + i);
     }
-    __device__ __forceinline__ static f32x4 ldf(const float *p, uint64_t i, uint32_t cnt, bool nt = false) {
-        if constexpr (VEC) {
-            return nt ? __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p + i))
-                      : *reinterpret_cast<const f32x4 *>(p + i);
-        } else {
-            f32x4 v = {0, 0, 0, 0};
-#pragma unroll
-            for (uint32_t j = 0; j < 4; ++j)
-                if (j < cnt) v[j] = p[i + j];
-            return v;
-        }
+    __device__ __forceinline__ static void stf(float *p, uint64_t i, f32x4 v, uint32_t, bool nt = false) {
+        if (nt)
+            __builtin_nontemporal_store(v, reinterpret_cast<f32x4 *>(p + i));
+        else
+            *reinterpret_cast<f32x4 *>(p + i) = v;
     }
-    __device__ __forceinline__ static void stf(float *p, uint64_t i, f32x4 v, uint32_t cnt, bool nt = false) {
-        if constexpr (VEC) {
-            if (nt)
-                __builtin_nontemporal_store(v, reinterpret_cast<f32x4 *>(p + i));
-            else
-                *reinterpret_cast<f32x4 *>(p + i) = v;
-        } else {
-#pragma unroll
-            for (uint32_t j = 0; j < 4; ++j)
-                if (j < cnt) p[i + j] = v[j];
+    __device__ __forceinline__ static void sth(half_t *p, uint64_t i, f32x4 v, uint32_t) {
+        store4<half_t>(p, i, v);
+    }
+};
+
+// Rows at any alignment (n % 4 != 0, or buffers not 16-byte aligned): the group
+// of elements i .. i + cnt - 1 of an array p is read as the aligned 4-element
+// chunk holding element i plus, when the group runs into the next chunk, that
+// chunk too.  Each chunk read holds an element of the group, so no read leaves
+// the 16-byte blocks the group's own elements lie in.  Stores split the group at
+// the chunk boundary into aligned 1-, 2- and 4-element pieces.  For a row-
+// strided group (first column a multiple of 4) the offset o of element i in its
+// chunk is the same in every lane of the row, so the switches on o branch
+// uniformly; only the lane that holds a row's last, partial group (cnt < 4)
+// takes the element-by-element path.
+template <typename T> struct GrpUA {
+    __device__ __forceinline__ static uint32_t lead(const void *p) {
+        return (uint32_t)((reinterpret_cast<uintptr_t>(p) / sizeof(T)) & 3u);
+    }
+    // Elements o .. o + 3 of the 8-element concatenation (a, b), o in 1..3.
+    // Written as selects: a switch returning the four vectors gave wrong
+    // elements for o = 3 inside the error kernel's unrolled row loop (hipcc,
+    // ROCm 7.2), while the same switch in a stand-alone loop did not.
+    __device__ __forceinline__ static f32x4 pick(f32x4 a, f32x4 b, uint32_t o) {
+        const bool o1 = o == 1, o2 = o == 2;
+        return f32x4{o1 ? a[1] : o2 ? a[2] : a[3], o1 ? a[2] : o2 ? a[3] : b[0], o1 ? a[3] : o2 ? b[0] : b[1],
+                     o1 ? b[0] : o2 ? b[1] : b[2]};
+    }
+    template <typename E> __device__ __forceinline__ static f32x4 load(const void *p, uint64_t i, uint32_t cnt) {
+        const uint32_t b = GrpUA<E>::lead(p);
+        const E *q = reinterpret_cast<const E *>(p) - b;   // 4-element aligned
+        const uint64_t k = i + b, ch = k & ~3ull;
+        const uint32_t o = (uint32_t)(k & 3u);
+        const f32x4 lo = load4<E>(q, ch);
+        if (o == 0) return lo;
+        const f32x4 hi = cnt > 4u - o ? load4<E>(q, ch + 4) : f32x4{0, 0, 0, 0};
+        return pick(lo, hi, o);
+    }
+    __device__ __forceinline__ static f32x4 ld(const void *p, uint64_t i, uint32_t cnt) { return load<T>(p, i, cnt); }
+    __device__ __forceinline__ static f32x4 ldf(const float *p, uint64_t i, uint32_t cnt, bool = false) {
+        return load<float>(p, i, cnt);
+    }
+    __device__ __forceinline__ static void stf(float *p, uint64_t i, f32x4 v, uint32_t cnt, bool = false) {
+        if (cnt < 4) {
+            for (uint32_t j = 0; j < cnt; ++j) p[i + j] = v[j];
+            return;
+        }
+        const uint32_t b = GrpUA<float>::lead(p);
+        float *q = p - b;
+        const uint64_t k = i + b, ch = k & ~3ull;
+        typedef float f32x2 __attribute__((ext_vector_type(2)));
+        switch ((uint32_t)(k & 3u)) {
+        case 0: *reinterpret_cast<f32x4 *>(q + ch) = v; break;
+        case 1:
+            q[ch + 1] = v[0];
+            *reinterpret_cast<f32x2 *>(q + ch + 2) = f32x2{v[1], v[2]};
+            q[ch + 4] = v[3];
+            break;
+        case 2:
+            *reinterpret_cast<f32x2 *>(q + ch + 2) = f32x2{v[0], v[1]};
+            *reinterpret_cast<f32x2 *>(q + ch + 4) = f32x2{v[2], v[3]};
+            break;
+        default:
+            q[ch + 3] = v[0];
+            *reinterpret_cast<f32x2 *>(q + ch + 4) = f32x2{v[1], v[2]};
+            q[ch + 6] = v[3];
+            break;
         }
     }
     __device__ __forceinline__ static void sth(half_t *p, uint64_t i, f32x4 v, uint32_t cnt) {
-        if constexpr (VEC) {
-            store4<half_t>(p, i, v);
-        } else {
-#pragma unroll
-            for (uint32_t j = 0; j < 4; ++j)
-                if (j < cnt) p[i + j] = (half_t)v[j];
+        if (cnt < 4) {
+            for (uint32_t j = 0; j < cnt; ++j) p[i + j] = (half_t)v[j];
+            return;
+        }
+        const uint32_t b = GrpUA<half_t>::lead(p);
+        half_t *q = p - b;
+        const uint64_t k = i + b, ch = k & ~3ull;
+        typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+        const half_t h0 = (half_t)v[0], h1 = (half_t)v[1], h2 = (half_t)v[2], h3 = (half_t)v[3];
+        switch ((uint32_t)(k & 3u)) {
+        case 0: *reinterpret_cast<f16x4 *>(q + ch) = f16x4{h0, h1, h2, h3}; break;
+        case 1:
+            q[ch + 1] = h0;
+            *reinterpret_cast<f16x2 *>(q + ch + 2) = f16x2{h1, h2};
+            q[ch + 4] = h3;
+            break;
+        case 2:
+            *reinterpret_cast<f16x2 *>(q + ch + 2) = f16x2{h0, h1};
+            *reinterpret_cast<f16x2 *>(q + ch + 4) = f16x2{h2, h3};
+            break;
+        default:
+            q[ch + 3] = h0;
+            *reinterpret_cast<f16x2 *>(q + ch + 4) = f16x2{h1, h2};
+            q[ch + 6] = h3;
+            break;
         }
     }
+};
+// GrpUA with the offset O of element i in its chunk known at compile time and
+// 4-element-aligned base pointers: no branches on the offset, and the picks
+// are register moves.
+template <typename T, int O> struct GrpUS {
+    template <typename E> __device__ __forceinline__ static f32x4 load(const void *p, uint64_t i, uint32_t cnt) {
+        const f32x4 lo = load4<E>(p, i - O);
+        if constexpr (O == 0) {
+            return lo;
+        } else {
+            const f32x4 hi = cnt > 4u - O ? load4<E>(p, i - O + 4) : f32x4{0, 0, 0, 0};
+            if constexpr (O == 1) return f32x4{lo[1], lo[2], lo[3], hi[0]};
+            if constexpr (O == 2) return f32x4{lo[2], lo[3], hi[0], hi[1]};
+            return f32x4{lo[3], hi[0], hi[1], hi[2]};
+        }
+    }
+    __device__ __forceinline__ static f32x4 ld(const void *p, uint64_t i, uint32_t cnt) { return load<T>(p, i, cnt); }
+    __device__ __forceinline__ static f32x4 ldf(const float *p, uint64_t i, uint32_t cnt, bool = false) {
+        return load<float>(p, i, cnt);
+    }
+    template <typename E, typename V2> __device__ __forceinline__ static void put(E *q, f32x4 v) {
+        // q = the group's first element; pieces at the chunk boundary
+        if constexpr (O == 0) {
+            if constexpr (sizeof(E) == 4)
+                *reinterpret_cast<f32x4 *>(q) = v;
+            else
+                *reinterpret_cast<f16x4 *>(q) = f16x4{(E)v[0], (E)v[1], (E)v[2], (E)v[3]};
+        } else if constexpr (O == 2) {
+            *reinterpret_cast<V2 *>(q) = V2{(E)v[0], (E)v[1]};
+            *reinterpret_cast<V2 *>(q + 2) = V2{(E)v[2], (E)v[3]};
+        } else {
+            q[0] = (E)v[0];
+            *reinterpret_cast<V2 *>(q + 1) = V2{(E)v[1], (E)v[2]};
+            q[3] = (E)v[3];
+        }
+    }
+    __device__ __forceinline__ static void stf(float *p, uint64_t i, f32x4 v, uint32_t cnt, bool = false) {
+        typedef float f32x2 __attribute__((ext_vector_type(2)));
+        if (cnt < 4) {
+            for (uint32_t j = 0; j < cnt; ++j) p[i + j] = v[j];
+            return;
+        }
+        put<float, f32x2>(p + i, v);
+    }
+    __device__ __forceinline__ static void sth(half_t *p, uint64_t i, f32x4 v, uint32_t cnt) {
+        typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+        if (cnt < 4) {
+            for (uint32_t j = 0; j < cnt; ++j) p[i + j] = (half_t)v[j];
+            return;
+        }
+        put<half_t, f16x2>(p + i, v);
+    }
+};
+
+// Accessor modes of the error kernels: 1 = GrpV (n % 4 == 0, aligned buffers);
+// 4 + n % 4 = GrpUS (aligned buffers, n % 4 != 0, row splits a multiple of 4
+// rows, so row rb + u with rb % 4 == 0 starts at offset (u n) % 4 of its
+// chunk); 0 = GrpUA (anything else).  RowAcc: the row-strided [rows x n]
+// arrays of row slot u; ColAcc: per-column vectors and the supplied sum s.
+template <typename T, int MODE, int U> struct RowAcc {
+    typedef typename std::conditional<
+        MODE == 1, GrpV<T>,
+        typename std::conditional<MODE == 0, GrpUA<T>, GrpUS<T, (U * (MODE - 4)) & 3>>::type>::type type;
+};
+template <typename T, int MODE> struct ColAcc {
+    typedef typename std::conditional<MODE == 0, GrpUA<T>, GrpV<T>>::type type;
 };
 
 // The three values of one 4-column group that feed the column sums of backward.cu:187-194.
@@ -423,10 +556,9 @@ struct ErrSums4 {
 
 // grad = e; the element-local norm gradient (util.cu:175-215) into d_prenorm and
 // dNorm; d_prenorm scaled by the loss scale; its fp16 copy for the GEMMs.
-template <typename T, bool VEC>
+template <typename T, class G, class GC>
 __device__ __forceinline__ ErrSums4 write_err4(const ErrArgs &a, uint64_t idx, uint32_t row, uint32_t col,
                                                uint32_t cnt, f32x4 e) {
-    typedef Grp<T, VEC> G;
     G::stf(a.grad, idx, e, cnt, true);
     ErrSums4 o;
     o.dp = e;
@@ -434,7 +566,7 @@ __device__ __forceinline__ ErrSums4 write_err4(const ErrArgs &a, uint64_t idx, u
     if (a.norm) {
         const f32x4 pv = a.norm == 1 ? G::ld(a.prenorm, idx, cnt) : f32x4{0, 0, 0, 0};
         const f32x4 cv = a.norm >= 2 ? G::ld(a.centered, idx, cnt) : f32x4{0, 0, 0, 0};
-        const f32x4 nw = G::ldf(a.nw, col, cnt);
+        const f32x4 nw = GC::ldf(a.nw, col, cnt);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const float rstd = to_f32(ldv<T>(a.norm_rstd, a.norm == 3 ? col + (j < (int)cnt ? j : 0) : row));
@@ -449,7 +581,7 @@ __device__ __forceinline__ ErrSums4 write_err4(const ErrArgs &a, uint64_t idx, u
     o.dp = o.dp * a.loss_scale;
     G::stf(a.d_prenorm, idx, o.dp, cnt, true);
     if (a.d_prenorm_h) G::sth(a.d_prenorm_h, idx, o.dp, cnt);
-    if (!VEC) {
+    if (cnt < 4) {
         // columns past n add nothing to the sums
 #pragma unroll
         for (uint32_t j = 0; j < 4; ++j)
@@ -459,9 +591,8 @@ __device__ __forceinline__ ErrSums4 write_err4(const ErrArgs &a, uint64_t idx, u
 }
 
 // Loss delta of one 4-column group (backward.cu:24-45).
-template <typename T, bool VEC>
+template <typename T, class G>
 __device__ __forceinline__ f32x4 output_err4(const ErrArgs &a, uint64_t idx, uint32_t cnt) {
-    typedef Grp<T, VEC> G;
     const f32x4 out = G::ld(a.out, idx, cnt), tg = G::ld(a.target, idx, cnt), pre = G::ld(a.preact, idx, cnt);
     f32x4 e;
 #pragma unroll
@@ -491,91 +622,124 @@ __device__ __forceinline__ f32x4 output_err4(const ErrArgs &a, uint64_t idx, uin
 // measured on the C3 step (rows x column groups per thread in {4x1, 2x2, 1x4,
 // 2x4}, 512 to 2048 workgroups) the fastest, both alone and between the GEMMs.
 constexpr int ERR_UR = 4;
-// Without VEC a thread owns one column (cnt = 1) instead: consecutive lanes
-// read consecutive elements, whatever the rows' alignment.
-template <typename T, bool FROM_SUM, bool VEC>
+struct ErrAcc {   // running column sums of one 4-column group
+    f32x4 dp, nw, nb;
+};
+template <typename T, bool FROM_SUM, int MODE, int U>
+__device__ __forceinline__ void err_load(const ErrArgs &a, uint32_t rb, uint32_t r1, uint32_t c, uint32_t cnt,
+                                         uint32_t s_ld, f32x4 (&x)[4][ERR_UR]) {
+    typedef typename RowAcc<T, MODE, U>::type G;
+    typedef typename ColAcc<float, MODE>::type GS;
+    if (rb + U >= r1) return;
+    const uint64_t idx = (uint64_t)(rb + U) * a.n + c;
+    x[0][U] = GS::ldf(a.s, (uint64_t)(rb + U) * s_ld + c, cnt, true);
+    x[1][U] = G::ld(a.predrop, idx, cnt);
+    x[2][U] = G::ld(a.preact, idx, cnt);
+    x[3][U] = G::ld(a.mask, idx, cnt);
+}
+template <typename T, bool FROM_SUM, int MODE, int U>
+__device__ __forceinline__ void err_row(const ErrArgs &a, uint32_t rb, uint32_t r1, uint32_t c, uint32_t cnt,
+                                        const f32x4 (&x)[4][ERR_UR], ErrAcc &acc) {
+    typedef typename RowAcc<T, MODE, U>::type G;
+    typedef typename ColAcc<float, MODE>::type GC;
+    const uint32_t row = rb + U;
+    if (row >= r1) return;
+    const uint64_t idx = (uint64_t)row * a.n + c;
+    f32x4 e;
+    if constexpr (FROM_SUM) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            e[j] = x[3][U][j] * activation_derivative(a.act, x[0][U][j], x[1][U][j], x[2][U][j], a.leaky);
+    } else {
+        e = output_err4<T, G>(a, idx, cnt);
+    }
+    const ErrSums4 o = write_err4<T, G, GC>(a, idx, row, c, cnt, e);
+    acc.dp += o.dp;
+    acc.nw += o.dnw;
+    acc.nb += o.dnb;
+}
+template <typename T, bool FROM_SUM, int MODE, int... U>
+__device__ __forceinline__ void err_rows(const ErrArgs &a, uint32_t rb, uint32_t r1, uint32_t c, uint32_t cnt,
+                                         uint32_t s_ld, ErrAcc &acc, std::integer_sequence<int, U...>) {
+    f32x4 x[4][ERR_UR];
+    if constexpr (FROM_SUM) (err_load<T, FROM_SUM, MODE, U>(a, rb, r1, c, cnt, s_ld, x), ...);
+    (err_row<T, FROM_SUM, MODE, U>(a, rb, r1, c, cnt, x, acc), ...);
+}
+template <typename T, bool FROM_SUM, int MODE>
 __global__ void __launch_bounds__(256) error_cols_kernel(ErrArgs a, float *__restrict__ partials, uint32_t per) {
-    typedef Grp<T, VEC> G;
-    const uint32_t c = VEC ? blockIdx.x * 1024 + threadIdx.x * 4 : blockIdx.x * 256 + threadIdx.x;
+    const uint32_t c = blockIdx.x * 1024 + threadIdx.x * 4;
     if (c >= a.n) return;
-    const uint32_t cnt = VEC ? min(4u, a.n - c) : 1u;
+    const uint32_t cnt = min(4u, a.n - c);
     const uint32_t s_ld = a.s_ld ? a.s_ld : a.n;
     const uint32_t r0 = blockIdx.y * per;
     const uint32_t r1 = min(a.rows, r0 + per);
-    f32x4 sdp = {0, 0, 0, 0}, snw = {0, 0, 0, 0}, snb = {0, 0, 0, 0};
-    for (uint32_t rb = r0; rb < r1; rb += ERR_UR) {
-        f32x4 x0[ERR_UR], x1[ERR_UR], x2[ERR_UR], x3[ERR_UR];
-        if constexpr (FROM_SUM) {
-#pragma unroll
-            for (int u = 0; u < ERR_UR; ++u) {
-                if (rb + u >= r1) break;
-                const uint64_t idx = (uint64_t)(rb + u) * a.n + c;
-                x0[u] = G::ldf(a.s, (uint64_t)(rb + u) * s_ld + c, cnt, true);
-                x1[u] = G::ld(a.predrop, idx, cnt);
-                x2[u] = G::ld(a.preact, idx, cnt);
-                x3[u] = G::ld(a.mask, idx, cnt);
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < ERR_UR; ++u) {
-            const uint32_t row = rb + u;
-            if (row >= r1) break;
-            const uint64_t idx = (uint64_t)row * a.n + c;
-            f32x4 e;
-            if constexpr (FROM_SUM) {
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    e[j] = x3[u][j] * activation_derivative(a.act, x0[u][j], x1[u][j], x2[u][j], a.leaky);
-            } else {
-                e = output_err4<T, VEC>(a, idx, cnt);
-            }
-            const ErrSums4 o = write_err4<T, VEC>(a, idx, row, c, cnt, e);
-            sdp += o.dp;
-            snw += o.dnw;
-            snb += o.dnb;
-        }
-    }
+    ErrAcc acc{{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
+    for (uint32_t rb = r0; rb < r1; rb += ERR_UR)
+        err_rows<T, FROM_SUM, MODE>(a, rb, r1, c, cnt, s_ld, acc, std::make_integer_sequence<int, ERR_UR>{});
+    typedef typename std::conditional<MODE == 1, GrpV<float>, GrpUA<float>>::type GP;
     float *p = partials + (uint64_t)blockIdx.y * 3 * a.n + c;
-    G::stf(p, 0, sdp, cnt);
+    GP::stf(p, 0, acc.dp, cnt);
     if (a.norm) {
-        G::stf(p + a.n, 0, snw, cnt);
-        G::stf(p + 2 * a.n, 0, snb, cnt);
+        GP::stf(p + a.n, 0, acc.nw, cnt);
+        GP::stf(p + 2 * a.n, 0, acc.nb, cnt);
     }
 }
 
 static bool a16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-static bool err_vec_ok(const ErrArgs &a, bool from_sum, const float *partials) {
-    if ((a.n & 3u) != 0 || (from_sum && (a.s_ld & 3u) != 0)) return false;
+// Every buffer the kernel touches 16-byte aligned, and s's rows a multiple of 4
+// elements apart (partials only matter for GrpV: GrpUS writes them via GrpUA).
+static bool err_aligned(const ErrArgs &a, bool from_sum, const float *partials) {
+    if (from_sum && (a.s_ld & 3u) != 0) return false;
     const void *ptrs[] = {a.grad, a.d_prenorm, a.d_prenorm_h, a.preact, a.norm ? a.nw : nullptr,
                           a.norm ? a.d_norm_w : nullptr, a.norm ? a.d_norm_b : nullptr,
                           a.norm == 1 ? a.prenorm : nullptr, a.norm >= 2 ? a.centered : nullptr,
                           from_sum ? a.s : a.out, from_sum ? a.predrop : a.target, from_sum ? a.mask : nullptr,
-                          partials};
+                          (a.n & 3u) == 0 ? partials : nullptr};
     for (const void *p : ptrs)
         if (p && !a16(p)) return false;
     return true;
 }
 
-// Row splits of the error kernels: ~1024 workgroups.
+// Row splits of the error kernels: ~1024 workgroups of >= 16 rows for n >= 1024;
+// narrower outputs leave most of a workgroup's 256 column-group lanes idle, so
+// they get ~256K active lanes in all, in slices of >= 4 rows (at most 4096).
 uint32_t err_col_splits(uint32_t rows, uint32_t n) {
-    const uint32_t col_blocks = cdiv(n, 1024);
-    uint32_t sp = cdiv(1024, col_blocks);
-    const uint32_t cap = cdiv(rows, 16);
+    uint32_t sp, cap;
+    if (n >= 1024) {
+        sp = cdiv(1024, cdiv(n, 1024));
+        cap = cdiv(rows, 16);
+    } else {
+        sp = cdiv(262144u, cdiv(n, 4));
+        cap = cdiv(rows, 4);
+    }
     if (sp > cap) sp = cap;
-    if (sp > 1024) sp = 1024;
+    if (sp > 4096) sp = 4096;
     return sp < 1 ? 1 : sp;
+}
+
+template <bool FROM_SUM, typename T, int MODE>
+static void launch_error_mode(const ErrArgs &a, float *partials, uint32_t splits, uint32_t per, hipStream_t s) {
+    hipLaunchKernelGGL((error_cols_kernel<T, FROM_SUM, MODE>), dim3(cdiv(a.n, 1024), splits), dim3(256), 0, s, a,
+                       partials, per);
 }
 
 template <bool FROM_SUM, typename T>
 static void launch_error_t(const ErrArgs &a, float *partials, uint32_t splits, hipStream_t s) {
     const uint32_t per = cdiv(a.rows, splits);
-    if (err_vec_ok(a, FROM_SUM, partials))
-        hipLaunchKernelGGL((error_cols_kernel<T, FROM_SUM, true>), dim3(cdiv(a.n, 1024), splits), dim3(256), 0, s,
-                           a, partials, per);
-    else
-        hipLaunchKernelGGL((error_cols_kernel<T, FROM_SUM, false>), dim3(cdiv(a.n, 256), splits), dim3(256), 0, s,
-                           a, partials, per);
+    if (!err_aligned(a, FROM_SUM, partials)) {
+        launch_error_mode<FROM_SUM, T, 0>(a, partials, splits, per, s);
+        return;
+    }
+    // GrpUS needs every row slice to start on a multiple of 4 rows; the last
+    // slices may then be empty (their partial sums are zeros)
+    const uint32_t per4 = (per + 3u) & ~3u;
+    switch (a.n & 3u) {
+    case 0: launch_error_mode<FROM_SUM, T, 1>(a, partials, splits, per, s); break;
+    case 1: launch_error_mode<FROM_SUM, T, 5>(a, partials, splits, per4, s); break;
+    case 2: launch_error_mode<FROM_SUM, T, 6>(a, partials, splits, per4, s); break;
+    default: launch_error_mode<FROM_SUM, T, 7>(a, partials, splits, per4, s); break;
+    }
 }
 
 hipError_t launch_output_error(const ErrArgs &a, float *partials, uint32_t splits, hipStream_t s) {

@@ -127,12 +127,13 @@ void   *skl_ctx_stream(skl_ctx *ctx);
 int32_t skl_synchronize(skl_ctx *ctx);
 /* Human-readable name of a status code. */
 const char *skl_status_string(int32_t status);
-/* Measurement aid, no counterpart in the reference: record start_event and
- * stop_event (hipEvent_t, created by the caller) on the context's stream
- * around the GEMM kernel of the next DenseBlock call that launches one (the
- * GEMM alone: not the operand staging, element-wise or reduction kernels
- * around it); the hook then clears itself.  NULL, NULL clears it.  Not an
- * entry-point call in the sense of skl_dense_backward's column-sum reuse. */
+/* Measurement aid, no counterpart in the reference: the GEMM kernel of the
+ * next DenseBlock call that launches one records start_event and stop_event
+ * (hipEvent_t, created by the caller) at its own start and end, through its
+ * dispatch (no marker packets enter the stream); the GEMM alone, not the
+ * operand staging, element-wise or reduction kernels around it.  The hook then
+ * clears itself.  NULL, NULL clears it.  Not an entry-point call in the sense
+ * of skl_dense_backward's column-sum reuse. */
 int32_t skl_ctx_time_next_gemm(skl_ctx *ctx, void *start_event, void *stop_event);
 
 /* ---- memory (replaces cudarc CudaSlice alloc/copy used by core.rs:557-692) -- */

@@ -156,7 +156,9 @@ class Context:
         call("skl_ctx_set_stream", self.h, C.c_void_p(stream_ptr) if stream_ptr else None)
 
     def time_next_gemm(self, start, stop):
-        """Record two torch.cuda.Event objects around the GEMM kernel of the next hot-path call."""
+        """Record two torch.cuda.Event objects at the start and end of the GEMM kernel of the next
+        hot-path call (torch creates an event's HIP object on its first record(), so record each
+        once beforehand)."""
         call("skl_ctx_time_next_gemm", self.h, C.c_void_p(start.cuda_event), C.c_void_p(stop.cuda_event))
 
     def set_sync(self, sync: bool):

@@ -220,24 +220,21 @@ GemmPlan plan_gemm(const GemmLaunch &g) {
 
 enum class GemmKind { Dma, Staged, SkinnyFwd, SkinnyDw };
 
-// One GEMM launch, bracketed by the events of skl_ctx_time_next_gemm when set.
-hipError_t timed_gemm(skl_ctx *ctx, const GemmLaunch &g, GemmKind kind, float *partials = nullptr,
+// One GEMM launch; when skl_ctx_time_next_gemm armed a pair of events, the GEMM
+// kernel's own dispatch records them (no marker packets in the stream).
+hipError_t timed_gemm(skl_ctx *ctx, const GemmLaunch &g0, GemmKind kind, float *partials = nullptr,
                       uint32_t slices = 0) {
-    hipEvent_t stop = ctx->gemm_stop;
-    if (ctx->gemm_start) {
-        const hipError_t e = hipEventRecord(ctx->gemm_start, ctx->stream);
-        ctx->gemm_start = ctx->gemm_stop = nullptr;
-        if (e != hipSuccess) return e;
-    }
-    hipError_t e = hipSuccess;
+    GemmLaunch g = g0;
+    g.time_start = ctx->gemm_start;
+    g.time_stop = ctx->gemm_stop;
+    ctx->gemm_start = ctx->gemm_stop = nullptr;
     switch (kind) {
-    case GemmKind::Dma: e = launch_gemm_dma(g, ctx->stream); break;
-    case GemmKind::Staged: e = launch_gemm(g, ctx->stream); break;
-    case GemmKind::SkinnyFwd: e = launch_skinny_fwd(g, ctx->stream); break;
-    case GemmKind::SkinnyDw: e = launch_skinny_dw(g, partials, slices, ctx->stream); break;
+    case GemmKind::Dma: return launch_gemm_dma(g, ctx->stream);
+    case GemmKind::Staged: return launch_gemm(g, ctx->stream);
+    case GemmKind::SkinnyFwd: return launch_skinny_fwd(g, ctx->stream);
+    case GemmKind::SkinnyDw: return launch_skinny_dw(g, partials, slices, ctx->stream);
     }
-    if (e != hipSuccess) return e;
-    return stop ? hipEventRecord(stop, ctx->stream) : hipSuccess;
+    return hipSuccess;
 }
 
 // Runs g as planned; ws holds plan.bytes() of workspace.  full_out: the output

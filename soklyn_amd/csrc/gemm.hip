@@ -2,11 +2,24 @@
 // contractions (forward, dX, dW) on gfx950.
 #include <stdlib.h>
 
+#include <hip/hip_ext.h>
+
 #include "gemm.h"
 #include "gemm_dma.h"
 #include "launch.h"
 
 namespace skl {
+
+// Launches a GEMM kernel; with g.time_start / g.time_stop set, the dispatch
+// itself carries the timing events.
+template <typename K, typename... Args>
+static void launch_timed(const GemmLaunch &g, K kernel, dim3 grid, dim3 block, hipStream_t s, Args... args) {
+    if (g.time_start || g.time_stop)
+        hipExtLaunchKernelGGL(kernel, grid, block, 0, s, g.time_start, g.time_stop, 0, args...);
+    else
+        hipLaunchKernelGGL(kernel, grid, block, 0, s, args...);
+}
+
 
 template <typename T> __device__ __forceinline__ T ld_t(const void *p, uint64_t i) {
     return reinterpret_cast<const T *>(p)[i];
@@ -218,9 +231,8 @@ static hipError_t run(const GemmLaunch &g, const typename Epi::Params &p, hipStr
     const uint32_t kps_raw = (g.K + splits - 1) / splits;
     sh.k_per_split = ((kps_raw + C::bk - 1) / C::bk) * C::bk;
     dim3 grid(sh.tiles_m * sh.tiles_n, 1, splits);
-    hipLaunchKernelGGL((gemm_kernel<T, C::bm, C::bn, C::bk, C::wm, C::wn, AK, BK_, VOK, Epi>), grid,
-                       dim3(C::nt), 0, s, sh, reinterpret_cast<const T *>(g.A),
-                       reinterpret_cast<const T *>(g.B), p);
+    launch_timed(g, gemm_kernel<T, C::bm, C::bn, C::bk, C::wm, C::wn, AK, BK_, VOK, Epi>, grid, dim3(C::nt), s, sh,
+                 reinterpret_cast<const T *>(g.A), reinterpret_cast<const T *>(g.B), p);
     return hipGetLastError();
 }
 
@@ -364,11 +376,9 @@ static hipError_t run_dma(const GemmLaunch &g, const typename Epi::Params &p, ui
     const half_t *A = reinterpret_cast<const half_t *>(g.A);
     const half_t *B = reinterpret_cast<const half_t *>(g.B);
     if (dma_full_epilogue(g))
-        hipLaunchKernelGGL((gemm_dma_kernel<Epi, AK, BK_, NW, false>), grid, dim3(DmaCfg<NW>::NT), 0, s, sh, A, B,
-                           p);
+        launch_timed(g, gemm_dma_kernel<Epi, AK, BK_, NW, false>, grid, dim3(DmaCfg<NW>::NT), s, sh, A, B, p);
     else
-        hipLaunchKernelGGL((gemm_dma_kernel<Epi, AK, BK_, NW, true>), grid, dim3(DmaCfg<NW>::NT), 0, s, sh, A, B,
-                           p);
+        launch_timed(g, gemm_dma_kernel<Epi, AK, BK_, NW, true>, grid, dim3(DmaCfg<NW>::NT), s, sh, A, B, p);
     return hipGetLastError();
 }
 
@@ -498,9 +508,9 @@ template <typename T> static void launch_skinny_fwd_t(const GemmShape &sh, const
     if (grid > 256) grid = 256;
     const T *A = reinterpret_cast<const T *>(g.A), *B = reinterpret_cast<const T *>(g.B);
     if (vecx)
-        hipLaunchKernelGGL((skinny_fwd_kernel<T, true>), dim3(grid), dim3(1024), 0, s, sh, A, B, g.fwd);
+        launch_timed(g, skinny_fwd_kernel<T, true>, dim3(grid), dim3(1024), s, sh, A, B, g.fwd);
     else
-        hipLaunchKernelGGL((skinny_fwd_kernel<T, false>), dim3(grid), dim3(1024), 0, s, sh, A, B, g.fwd);
+        launch_timed(g, skinny_fwd_kernel<T, false>, dim3(grid), dim3(1024), s, sh, A, B, g.fwd);
 }
 
 hipError_t launch_skinny_fwd(const GemmLaunch &g, hipStream_t s) {
@@ -577,11 +587,11 @@ hipError_t launch_skinny_dw(const GemmLaunch &g, float *partials, uint32_t slice
     const uint32_t per = (g.K + slices - 1) / slices;
     const dim3 grid((g.M + 255) / 256, slices);
     if (g.dtype == 1)
-        hipLaunchKernelGGL(skinny_dw_kernel<half_t>, grid, dim3(256), 0, s, sh,
-                           reinterpret_cast<const half_t *>(g.A), g.b32, partials, per);
+        launch_timed(g, skinny_dw_kernel<half_t>, grid, dim3(256), s, sh, reinterpret_cast<const half_t *>(g.A),
+                     g.b32, partials, per);
     else
-        hipLaunchKernelGGL(skinny_dw_kernel<float>, grid, dim3(256), 0, s, sh,
-                           reinterpret_cast<const float *>(g.A), g.b32, partials, per);
+        launch_timed(g, skinny_dw_kernel<float>, grid, dim3(256), s, sh, reinterpret_cast<const float *>(g.A),
+                     g.b32, partials, per);
     return hipGetLastError();
 }
 

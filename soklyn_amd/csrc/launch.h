@@ -55,6 +55,9 @@ struct GemmLaunch {
     OptEpi opt;
     StoreEpi st;
     const float *b32;     // dW: fp32 d_prenorm (ld N), read by the skinny kernel instead of B
+    // When set, the GEMM kernel's own dispatch records these events at its start
+    // and end (hipExtLaunchKernelGGL: no marker packets between kernels).
+    hipEvent_t time_start, time_stop;
 };
 
 hipError_t launch_gemm(const GemmLaunch &g, hipStream_t stream);

@@ -103,3 +103,24 @@ def test_backward_padded_and_split(ctx, M, K, N, norm):
     if norm:
         check("dm_norm_w", db.get("dm_norm_w"), ob.dm_norm_w, FP16_TOL)
     assert np.array_equal(db.get("w"), db.get("master_w").astype(np.float16).astype(np.float32))
+
+
+@pytest.mark.parametrize("M,K,N", [(2048, 1024, 1024), (333, 200, 150)])
+def test_gemm_timing_hook(ctx, M, K, N):
+    """skl_ctx_time_next_gemm: the next GEMM kernel's dispatch records the two events
+    (the 256x256 kernel, then the register-staged one); the call's results are unchanged."""
+    print(f"timing hook {M}x{K}x{N}", flush=True)
+    ob, db = make_pair(ctx, K, N, M, seed=5, half=True, act=abi.ACT_SILU)
+    x = inputs(6, M, K, True)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()   # torch creates its HIP events on first record
+    stop.record()
+    torch.cuda.synchronize()
+    ctx.time_next_gemm(start, stop)
+    ob.forward(x, M)
+    db.forward(dev(x, True), M)
+    stop.synchronize()
+    ms = start.elapsed_time(stop)
+    assert 0.0 < ms < 1000.0, f"GEMM time {ms} ms"
+    torch.cuda.synchronize()
+    check("out", db.get("out"), ob.out, FP16_TOL)

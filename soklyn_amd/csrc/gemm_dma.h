@@ -53,13 +53,35 @@
 
 namespace skl {
 
-template <int NW_> struct DmaCfg {
+template <int NW_, int MI_ = 32> struct DmaCfg {
     static_assert(NW_ == 4 || NW_ == 8, "4 or 8 waves");
-    static constexpr int NW = NW_;
+    static_assert(MI_ == 16 || MI_ == 32, "16x16x32 or 32x32x16 MFMA");
+    static constexpr int NW = NW_, MI = MI_;
     static constexpr int BM = 256, BN = 256, BK = 64, WM = 2, WN = NW / 2, NT = 64 * NW;
-    static constexpr int TWM = BM / WM, TWN = BN / WN, MT = TWM / 32, NTL = TWN / 32;
+    static constexpr int TWM = BM / WM, TWN = BN / WN, MT = TWM / MI, NTL = TWN / MI;
+    static constexpr int KSTEP = 512 / MI;         // k per MFMA
+    static constexpr int KS = BK / KSTEP;          // k-steps per tile
     static constexpr int OPB = 256 * BK * 2;       // 32 KB per operand tile
     static constexpr int STAGEB = 2 * OPB;         // 64 KB per stage
+};
+
+// One MFMA block; the B fragment (n rows) is the instruction's first operand and
+// the A fragment (m rows) its second, so a lane's accumulators are consecutive
+// n of one m.  32: lane l, register r holds (n = 8 (r / 4) + 4 (l / 32) + r % 4,
+// m = l % 32); 16: (n = 4 (l / 16) + r, m = l % 16).
+template <int MI> struct DmaMma;
+template <> struct DmaMma<32> {
+    typedef floatx16 Acc;
+    __device__ __forceinline__ static void run(Acc &acc, const u32x4 &bop, const u32x4 &aop) {
+        Mfma<half_t>::run(acc, bop, aop);
+    }
+};
+template <> struct DmaMma<16> {
+    typedef floatx4 Acc;
+    __device__ __forceinline__ static void run(Acc &acc, const u32x4 &bop, const u32x4 &aop) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(halfx8, bop), __builtin_bit_cast(halfx8, aop),
+                                                     acc, 0, 0, 0);
+    }
 };
 
 typedef __attribute__((address_space(3))) char lds_char;
@@ -115,8 +137,9 @@ __device__ __forceinline__ void pin(u32x2 &v) { asm volatile("" : "+v"(v)); }
 // chunks of 8 halves, chunk c of row r stored at slot c ^ ((r >> 1) & 7): any
 // 16 consecutive rows of one chunk column hit 16 distinct 16-byte bank groups.
 // A fragment is one ds_read_b128.
-template <int NW, int NF> struct OpK {
+template <int NW, int NF, int MI = 32> struct OpK {
     static constexpr int IPO = 32 / NW;   // DMA instructions per tile and wave
+    static constexpr uint32_t CPK = 512 / MI / 8;   // 16-byte chunks of a row per k-step
     struct Frag { u32x4 v[NF]; };
     DmaSrc dma;                       // DMA source of this lane, t = 0, k-tile 0
     uint32_t step;                    // bytes between DMA instructions (8 NW rows)
@@ -131,21 +154,27 @@ template <int NW, int NF> struct OpK {
         const uint32_t kc = (lane & 7u) ^ ((row0 >> 1) & 7u);
         dma.init(p, rows * ld * 2u, (mn0 + row0) * ld * 2u + kc * 16u);
         step = 8u * NW * ld * 2u;
-        const uint32_t frow = lane & 31u;
-        g = (lane >> 5) ^ ((frow >> 1) & 7u);
+        // wbase is a multiple of 32: the fragment row's swizzle is that of lane % MI
+        const uint32_t frow = lane % MI;
+        g = (lane / MI) ^ ((frow >> 1) & 7u);
         lds = lds_op + (wbase + frow) * 128u;
     }
     __device__ __forceinline__ void issue(int kt, int t, lds_char *dst) const {
         dma.load((uint32_t)kt * 128u + t * step, dst + t * (NW * 1024u));
     }
-    // fragment i: logical chunk 2 ks + (lane / 32) of row 32 i + lane % 32
+    // fragment i: logical chunk CPK ks + lane / MI of row MI i + lane % MI (the
+    // two terms have disjoint bits, so the swizzle XOR applies to them apart)
     __device__ __forceinline__ void read_frag(Frag &f, uint32_t stage_off, int ks, int i) const {
-        const uint32_t a = lds + stage_off + ((2u * ks) ^ g) * 16u;
+        const uint32_t a = lds + stage_off + ((CPK * ks) ^ g) * 16u;
         switch (i) {
         case 0: ds_read16<0>(f.v[0], a); break;
-        case 1: ds_read16<4096>(f.v[1], a); break;
-        case 2: if constexpr (NF > 2) ds_read16<8192>(f.v[2], a); break;
-        default: if constexpr (NF > 3) ds_read16<12288>(f.v[3], a); break;
+        case 1: ds_read16<1 * MI * 128>(f.v[1], a); break;
+        case 2: if constexpr (NF > 2) ds_read16<2 * MI * 128>(f.v[2], a); break;
+        case 3: if constexpr (NF > 3) ds_read16<3 * MI * 128>(f.v[3], a); break;
+        case 4: if constexpr (NF > 4) ds_read16<4 * MI * 128>(f.v[4], a); break;
+        case 5: if constexpr (NF > 5) ds_read16<5 * MI * 128>(f.v[5], a); break;
+        case 6: if constexpr (NF > 6) ds_read16<6 * MI * 128>(f.v[6], a); break;
+        default: if constexpr (NF > 7) ds_read16<7 * MI * 128>(f.v[7], a); break;
         }
     }
     __device__ __forceinline__ static u32x4 op(const Frag &f, int i) { return f.v[i]; }
@@ -165,37 +194,54 @@ template <int NW, int NF> struct OpK {
 // 4 distinct 64-byte bank windows.  Fragment i of the wave sits 32 rows
 // further on: chunk + 4 i, i.e. the lane's address XOR 64 i (the wave's first
 // row is a multiple of 32 NF, so the chunk bits that i flips start clear).
-template <int NW, int NF> struct OpN {
+template <int NW, int NF, int MI = 32> struct OpN {
     static constexpr int IPO = 32 / NW;
+    static constexpr uint32_t KSB = 512u * (512 / MI);   // bytes per k-step (KSTEP k-rows)
     struct Frag { u32x2 v[NF][2]; };
-    DmaSrc dma;
+    DmaSrc dma[2];                    // even / odd instructions (their swizzle differs for MI = 16, NW = 4)
     uint32_t step;                    // 2 NW k-rows per DMA instruction of a wave
     uint32_t kstep;                   // bytes per k-tile (64 k-rows)
-    uint32_t lds[NF];                 // per fragment i, stage 0, k-step 0, h = 0
+    uint32_t lds_op, rel;             // operand tile base; this lane's offset of fragment 0 (k-step 0, h = 0)
+
+    // MI = 16 adds 2 ((r >> 3) & 1): the two 16-lane groups of a half-wave read
+    // k-rows r and r + 8, which this moves to different banks
+    __device__ __forceinline__ static uint32_t swz(uint32_t r) {
+        return (4u * (r & 3u)) ^ (MI == 16 ? 2u * ((r >> 3) & 1u) : 0u);
+    }
 
     __device__ __forceinline__ void init(const half_t *p, uint32_t ld, uint32_t rows, uint32_t mn0, uint32_t wbase,
-                                         uint32_t wave, uint32_t lane, uint32_t lds_op) {
+                                         uint32_t wave, uint32_t lane, uint32_t lds_op_) {
         // instruction t (q = wave + NW t) fills k-rows 2 q, 2 q + 1; lane -> k-row 2 q + lane / 32,
-        // slot lane % 32; the swizzle term (k-row & 3) does not depend on t (NW is even)
-        const uint32_t r0 = 2u * wave + (lane >> 5);
-        const uint32_t cl = (lane & 31u) ^ (4u * (r0 & 3u));
-        dma.init(p, rows * ld * 2u, r0 * ld * 2u + mn0 * 2u + cl * 16u);
+        // slot lane % 32; r & 3 does not depend on t (NW is even), (r >> 3) & 1 only on t's parity
+#pragma unroll
+        for (uint32_t t = 0; t < 2; ++t) {
+            const uint32_t r = 2u * (wave + NW * t) + (lane >> 5);
+            const uint32_t cl = (lane & 31u) ^ swz(r);
+            dma[t].init(p, rows * ld * 2u, (2u * wave + (lane >> 5)) * ld * 2u + mn0 * 2u + cl * 16u);
+        }
         step = 2u * NW * ld * 2u;
         kstep = 64u * ld * 2u;
         const uint32_t grp = lane >> 4, s = lane & 15u;
-        const uint32_t row = 8u * (grp >> 1) + (s >> 2);
-        const uint32_t col = wbase + 16u * (grp & 1u) + 4u * (s & 3u);   // wbase % (32 NF) == 0
-        const uint32_t rel = row * 512u + (((col >> 3) ^ (4u * (row & 3u))) * 16u) + (col & 7u) * 2u;
-#pragma unroll
-        for (int i = 0; i < NF; ++i) lds[i] = lds_op + (rel ^ (64u * i));
+        uint32_t row, col;
+        if constexpr (MI == 32) {
+            row = 8u * (grp >> 1) + (s >> 2);
+            col = wbase + 16u * (grp & 1u) + 4u * (s & 3u);   // wbase % (32 NF) == 0
+        } else {
+            row = 8u * grp + (s >> 2);
+            col = wbase + 4u * (s & 3u);                      // wbase % (16 NF) == 0
+        }
+        rel = row * 512u + (((col >> 3) ^ swz(row)) * 16u) + (col & 7u) * 2u;
+        lds_op = lds_op_;
     }
     __device__ __forceinline__ void issue(int kt, int t, lds_char *dst) const {
-        dma.load((uint32_t)kt * kstep + t * step, dst + t * (NW * 1024u));
+        dma[t & 1].load((uint32_t)kt * kstep + t * step, dst + t * (NW * 1024u));
     }
-    // k-rows 16 ks + 4 h (+ 8): offsets 8192 ks + 2048 h keep the swizzle (multiples of 4 rows)
+    // fragment i sits MI rows further on: the lane's offset XOR 2 MI i; k-rows
+    // KSTEP ks + 4 h (+ 8 g) at offsets KSB ks + 2048 h keep the swizzle
     __device__ __forceinline__ void read_frag(Frag &f, uint32_t stage_off, int ks, int i) const {
-        ds_read8_tr<0>(f.v[i][0], lds[i] + stage_off + 8192u * ks);
-        ds_read8_tr<2048>(f.v[i][1], lds[i] + stage_off + 8192u * ks);
+        const uint32_t a = lds_op + (rel ^ (2u * MI * i)) + stage_off + KSB * ks;
+        ds_read8_tr<0>(f.v[i][0], a);
+        ds_read8_tr<2048>(f.v[i][1], a);
     }
     __device__ __forceinline__ static u32x4 op(const Frag &f, int i) {
         return u32x4{f.v[i][0].x, f.v[i][0].y, f.v[i][1].x, f.v[i][1].y};
@@ -209,24 +255,27 @@ template <int NW, int NF> struct OpN {
     }
 };
 
-template <bool KC, int NW, int NF> struct DmaOpSel { typedef OpK<NW, NF> type; };
-template <int NW, int NF> struct DmaOpSel<false, NW, NF> { typedef OpN<NW, NF> type; };
+template <bool KC, int NW, int NF, int MI> struct DmaOpSel { typedef OpK<NW, NF, MI> type; };
+template <int NW, int NF, int MI> struct DmaOpSel<false, NW, NF, MI> { typedef OpN<NW, NF, MI> type; };
 
 // Grid: (tiles, splits).  Split y reduces k in [y k_per_split, (y + 1) k_per_split)
 // (k_per_split a multiple of 128; the last split may be shorter, also a
 // multiple of 128).  EDGE: the operands are zero-padded copies whose M, N
 // extend past the real output [mv x nv]; the epilogue then goes element by
 // element through Epi::apply with those bounds (any leading dimension).
-template <class Epi, bool A_KC, bool B_KC, int NW, bool EDGE>
+template <class Epi, bool A_KC, bool B_KC, int NW, bool EDGE, int MI = 32>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4)))
     gemm_dma_kernel(GemmShape sh, const half_t *__restrict__ A, const half_t *__restrict__ B,
                     typename Epi::Params ep) {
-    typedef DmaCfg<NW> C;
-    typedef typename DmaOpSel<A_KC, NW, C::MT>::type OA;
-    typedef typename DmaOpSel<B_KC, NW, C::NTL>::type OB;
+    typedef DmaCfg<NW, MI> C;
+    typedef typename DmaOpSel<A_KC, NW, C::MT, MI>::type OA;
+    typedef typename DmaOpSel<B_KC, NW, C::NTL, MI>::type OB;
+    typedef DmaMma<MI> MM;
+    static_assert(C::KS % 2 == 0, "k-steps alternate between two fragment sets");
     constexpr int EPITCH = C::BN + 4;
-    constexpr int MTP = 2;                                   // accumulator rows per epilogue pass
-    constexpr int PROWS = C::WM * MTP * 32;
+    constexpr int RPP = 64;                                  // rows of a wave row per epilogue pass
+    constexpr int MTP = RPP / MI;                            // accumulator blocks per pass
+    constexpr int PROWS = C::WM * RPP;
     constexpr int EPI_BYTES = PROWS * EPITCH * 4;
     constexpr int MAIN_BYTES = 2 * C::STAGEB;
     __shared__ __attribute__((aligned(16))) char smem[MAIN_BYTES > EPI_BYTES ? MAIN_BYTES : EPI_BYTES];
@@ -236,8 +285,6 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
     const uint32_t lane = tid & 63u;
     const uint32_t wave = tid >> 6;
     const uint32_t wm = wave / C::WN, wn = wave % C::WN;
-    const uint32_t frow = lane & 31u;
-    const uint32_t fhalf = lane >> 5;
 
     uint32_t tm, tn;
     tile_coords(blockIdx.x, sh.tiles_m, sh.tiles_n, tm, tn);
@@ -261,13 +308,13 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
         for (int t = 0; t < OB::IPO; ++t) ob.issue(kt, t, st + C::OPB);
     };
 
-    floatx16 acc[C::MT][C::NTL];
+    typename MM::Acc acc[C::MT][C::NTL];
 #pragma unroll
     for (int i = 0; i < C::MT; ++i)
 #pragma unroll
         for (int j = 0; j < C::NTL; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+            for (int r = 0; r < (int)(sizeof(typename MM::Acc) / 4); ++r) acc[i][j][r] = 0.0f;
 
     typename OA::Frag fa[2];
     typename OB::Frag fb[2];
@@ -288,7 +335,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
     };
     auto mfma = [&](int set, int q) {
         const int i = q / C::NTL, j = q % C::NTL;
-        Mfma<half_t>::run(acc[i][j], OB::op(fb[set], j), OA::op(fa[set], i));
+        MM::run(acc[i][j], OB::op(fb[set], j), OA::op(fa[set], i));
     };
     auto dma = [&](int kt, int stage, int q) {
         lds_char *st = lsm + stage * C::STAGEB + wave * 1024u;
@@ -333,10 +380,9 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
             const int kt = kt0 + s;
-            kstep(0, s, 1);
-            kstep(1, s, 2);
-            kstep(0, s, 3);
-            // k-step 3 crosses the barrier: after it, MFMA q of set 1 is followed
+#pragma unroll
+            for (int ks = 0; ks + 1 < C::KS; ++ks) kstep(ks & 1, s, ks + 1);
+            // the last k-step (3) crosses the barrier: after it, MFMA q of set 1 is followed
             // by DMA instruction q of tile kt+2 (into the stage every wave has
             // just finished reading) and the reads of the next tile's k-step 0
             wait_vmcnt<0>();                    // this wave's DMA of tile kt+1 landed
@@ -379,20 +425,27 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
     const typename Epi::Params eps = Epi::at_split(ep, split);
     const typename Epi::Col col = EDGE ? typename Epi::Col{} : Epi::column(eps, n0 + c);
 #pragma unroll
-    for (int pass = 0; pass < C::MT / MTP; ++pass) {
+    for (int pass = 0; pass < C::TWM / RPP; ++pass) {
 #pragma unroll
         for (int ii = 0; ii < MTP; ++ii) {
             const int i = pass * MTP + ii;
-            const uint32_t r = (wm * MTP + ii) * 32 + frow;
 #pragma unroll
-            for (int j = 0; j < C::NTL; ++j)
+            for (int j = 0; j < C::NTL; ++j) {
+                if constexpr (MI == 32) {
+                    const uint32_t r = wm * RPP + ii * 32 + (lane & 31u);
 #pragma unroll
-                for (int gq = 0; gq < 4; ++gq) {
-                    const uint32_t cc = wn * C::TWN + j * 32 + gq * 8 + fhalf * 4;
-                    floatx4 v = {acc[i][j][4 * gq + 0], acc[i][j][4 * gq + 1], acc[i][j][4 * gq + 2],
-                                 acc[i][j][4 * gq + 3]};
-                    *reinterpret_cast<floatx4 *>(E + r * EPITCH + cc) = v;
+                    for (int gq = 0; gq < 4; ++gq) {
+                        const uint32_t cc = wn * C::TWN + j * 32 + gq * 8 + (lane >> 5) * 4;
+                        floatx4 v = {acc[i][j][4 * gq + 0], acc[i][j][4 * gq + 1], acc[i][j][4 * gq + 2],
+                                     acc[i][j][4 * gq + 3]};
+                        *reinterpret_cast<floatx4 *>(E + r * EPITCH + cc) = v;
+                    }
+                } else {
+                    const uint32_t r = wm * RPP + ii * 16 + (lane & 15u);
+                    const uint32_t cc = wn * C::TWN + j * 16 + (lane >> 4) * 4;
+                    *reinterpret_cast<floatx4 *>(E + r * EPITCH + cc) = acc[i][j];
                 }
+            }
         }
         lds_barrier();
         if constexpr (EDGE) {
@@ -403,8 +456,8 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
 #pragma unroll 1
             for (int b = 0; b < ROWS_PER_THREAD; ++b) {
                 const uint32_t r = wave + (uint32_t)NW * b;
-                const uint32_t wmi = r / (MTP * 32), rr = r % (MTP * 32);
-                const uint32_t m = m0 + wmi * C::TWM + pass * MTP * 32 + rr;
+                const uint32_t wmi = r / RPP, rr = r % RPP;
+                const uint32_t m = m0 + wmi * C::TWM + pass * RPP + rr;
                 if (m >= shv.M) continue;
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
@@ -416,7 +469,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
                     Epi::apply(ep, one, m, n, v, split);
                 }
             }
-            if (pass + 1 < C::MT / MTP) lds_barrier();
+            if (pass + 1 < C::TWM / RPP) lds_barrier();
             continue;
         }
 #pragma unroll 1
@@ -425,10 +478,10 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
             uint32_t mrow[EPI_BATCH];
 #pragma unroll
             for (int u = 0; u < EPI_BATCH; ++u) {
-                // E row r holds tile row wmi * TWM + pass * MTP * 32 + rr
+                // E row r holds tile row wmi * TWM + pass * RPP + rr
                 const uint32_t r = wave + (uint32_t)NW * (b + u);
-                const uint32_t wmi = r / (MTP * 32), rr = r % (MTP * 32);
-                mrow[u] = m0 + wmi * C::TWM + pass * MTP * 32 + rr;
+                const uint32_t wmi = r / RPP, rr = r % RPP;
+                mrow[u] = m0 + wmi * C::TWM + pass * RPP + rr;
                 Epi::load(eps, (uint64_t)mrow[u] * Epi::ldc(eps) + n0 + c, mrow[u], pre[u]);
             }
 #pragma unroll
@@ -438,7 +491,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
                 Epi::finish(eps, (uint64_t)mrow[u] * Epi::ldc(eps) + n0 + c, mrow[u], n0 + c, v, col, pre[u]);
             }
         }
-        if (pass + 1 < C::MT / MTP) lds_barrier();   // E is rewritten by the next pass
+        if (pass + 1 < C::TWM / RPP) lds_barrier();   // E is rewritten by the next pass
     }
 }
 

@@ -361,11 +361,11 @@ template <class Epi, bool AK, bool BK_>
 static hipError_t run_dma(const GemmLaunch &g, const typename Epi::Params &p, uint32_t splits, uint32_t kps,
                           hipStream_t s) {
     constexpr int NW = 8;
-    // v_mfma_f32_16x16x32_f16 for the all-k-contiguous layout (2% faster back to
-    // back, 5% with a cold last-level cache, on the C3 dX shape); 32x32x16 for
-    // the layouts with a transposed operand, whose 16x16 fragments at 8 waves
-    // overflow the register budget
-    constexpr int MI = (AK && BK_) ? 16 : 32;
+    // v_mfma_f32_16x16x32_f16 when A is k-contiguous (C3 shapes: dX 2% faster back
+    // to back, 5% with a cold last-level cache; forward 2-3%); 32x32x16 when both
+    // operands are transposed (dW), whose 16x16 fragments at 8 waves overflow the
+    // register budget even with A single-buffered
+    constexpr int MI = AK ? 16 : 32;
     GemmShape sh{};
     sh.M = g.M;
     sh.N = g.N;

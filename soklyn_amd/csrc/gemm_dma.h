@@ -3,6 +3,14 @@
 // m/n-contiguous (the forward's W, both operands of dW), so no layout needs a
 // transposed copy.
 //
+//  * MFMA shape MI = 32 (v_mfma_f32_32x32x16_f16, 32-row fragments) or 16
+//    (v_mfma_f32_16x16x32_f16, 16-row fragments, 32 k per MFMA).  A
+//    register-only loop of independent MFMAs on all 256 CUs sustains 2032
+//    TFLOP/s at 2.09 GHz with 16x16x32 and 1704 TFLOP/s at 1.68 GHz with
+//    32x32x16: the 16x16 form draws less power per flop.  With MI = 16 the A
+//    fragments are single-buffered (fragment i of the next k-step is read in
+//    place after its row's MFMAs), which keeps 8 waves inside the register
+//    budget when A is k-contiguous.
 //  * NW = 4 or 8 waves.  NW = 4: one wave per SIMD, wave tile 128 x 128 =
 //    4 x 4 v_mfma_f32_32x32x16_f16 blocks, 256 accumulators per lane in AGPRs;
 //    per k-step a wave reads 8 x 1 KB fragments for 16 MFMAs.  NW = 8: two
@@ -178,6 +186,8 @@ template <int NW, int NF, int MI = 32> struct OpK {
         }
     }
     __device__ __forceinline__ static u32x4 op(const Frag &f, int i) { return f.v[i]; }
+    static constexpr int RPF = 1;   // LDS reads per fragment
+    __device__ __forceinline__ static void pin_one(Frag &f, int i) { pin(f.v[i]); }
     __device__ __forceinline__ static void pin_all(Frag &f) {
 #pragma unroll
         for (int i = 0; i < NF; ++i) pin(f.v[i]);
@@ -245,6 +255,11 @@ template <int NW, int NF, int MI = 32> struct OpN {
     }
     __device__ __forceinline__ static u32x4 op(const Frag &f, int i) {
         return u32x4{f.v[i][0].x, f.v[i][0].y, f.v[i][1].x, f.v[i][1].y};
+    }
+    static constexpr int RPF = 2;   // LDS reads per fragment
+    __device__ __forceinline__ static void pin_one(Frag &f, int i) {
+        pin(f.v[i][0]);
+        pin(f.v[i][1]);
     }
     __device__ __forceinline__ static void pin_all(Frag &f) {
 #pragma unroll
@@ -368,6 +383,83 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
         }
     };
 
+    const int klast = kb + nk - 1;
+    if constexpr (MI == 16) {
+        // 16x16x32: A fragments single-buffered, B double-buffered.  A fragment i
+        // of the next k-step is read in place right after row i's MFMAs (its last
+        // use), the next k-step's B fragments behind row 0's MFMAs.  LDS reads
+        // complete in order; before row i the reads issued after A fragment i may
+        // still be pending: the other A fragments of its k-step plus, from row 1
+        // on, this k-step's B reads (capped at the counter's 15: stricter).
+        typename OA::Frag &fa1 = fa[0];
+        constexpr int W0 = (C::MT - 1) * OA::RPF < 15 ? (C::MT - 1) * OA::RPF : 15;
+        constexpr int W1 = (C::MT - 1) * OA::RPF + C::NTL * OB::RPF < 15
+                               ? (C::MT - 1) * OA::RPF + C::NTL * OB::RPF : 15;
+        auto mfma1 = [&](int set, int i, int j) { MM::run(acc[i][j], OB::op(fb[set], j), OA::op(fa1, i)); };
+        auto row_wait = [&](int cur, int i) {
+            if (i == 0) {
+                wait_lgkmcnt<W0>();
+                OB::pin_all(fb[cur]);
+            } else {
+                wait_lgkmcnt<W1>();
+            }
+            OA::pin_one(fa1, i);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        auto kstep1 = [&](int cur, int stage, int ks_next) {
+#pragma unroll
+            for (int i = 0; i < C::MT; ++i) {
+                row_wait(cur, i);
+#pragma unroll
+                for (int j = 0; j < C::NTL; ++j) {
+                    mfma1(cur, i, j);
+                    if (i == 0) ob.read_frag(fb[cur ^ 1], stage * C::STAGEB, ks_next, j);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                oa.read_frag(fa1, stage * C::STAGEB, ks_next, i);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
+        // prologue: tile 0 resident, tile 1 in flight; B fragments before A
+        // fragments, as in every later k-step
+        issue(kb, 0);
+        wait_vmcnt<0>();
+        __builtin_amdgcn_s_barrier();
+        issue(kb + (nk > 1 ? 1 : 0), 1);
+#pragma unroll
+        for (int j = 0; j < C::NTL; ++j) ob.read_frag(fb[0], 0, 0, j);
+#pragma unroll
+        for (int i = 0; i < C::MT; ++i) oa.read_frag(fa1, 0, 0, i);
+        for (int kt0 = 0; kt0 < nk; kt0 += 2) {
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                const int kt = kt0 + s;
+#pragma unroll
+                for (int ks = 0; ks + 1 < C::KS; ++ks) kstep1(ks & 1, s, ks + 1);
+                // the last k-step crosses the barrier: every read of stage s done
+                wait_vmcnt<0>();
+                wait_lgkmcnt<0>();
+                OB::pin_all(fb[1]);
+                OA::pin_all(fa1);
+                __builtin_amdgcn_s_barrier();
+                __builtin_amdgcn_sched_barrier(0);
+                const int kn = min(kb + kt + 2, klast);
+#pragma unroll
+                for (int i = 0; i < C::MT; ++i) {
+#pragma unroll
+                    for (int j = 0; j < C::NTL; ++j) {
+                        mfma1(1, i, j);
+                        const int q = i * C::NTL + j;
+                        if (q < NDMA) dma(kn, s, q);
+                        if (i == 0) ob.read_frag(fb[0], (s ^ 1) * C::STAGEB, 0, j);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                    oa.read_frag(fa1, (s ^ 1) * C::STAGEB, 0, i);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+        }
+    } else {
     // prologue: tile 0 resident, tile 1 in flight, first fragments read
     issue(kb, 0);
     wait_vmcnt<0>();
@@ -375,7 +467,6 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
     issue(kb + (nk > 1 ? 1 : 0), 1);
     read(0, 0, 0);
 
-    const int klast = kb + nk - 1;
     for (int kt0 = 0; kt0 < nk; kt0 += 2) {
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
@@ -400,6 +491,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
+    }
     }
     wait_vmcnt<0>();     // no DMA may land in the epilogue's staging area
     wait_lgkmcnt<0>();

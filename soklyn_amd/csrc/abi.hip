@@ -148,6 +148,31 @@ bool dma_operand_ok(const void *p, uint32_t rows, uint32_t cols, uint32_t ld, ui
     return rows % rows_mult == 0 && cols % cols_mult == 0 && ld % 8 == 0 && aligned16(p);
 }
 
+// Split-K slices for a dW grid of `tiles` 256x256 tiles over Kp (slices of at
+// least 512 k, at most 16): the count with the least estimated time, with one
+// workgroup per CU (256 CUs: a grid of w workgroups runs in ceil(w / 256)
+// rounds, each as long as one slice, ~3.4 us per 128 k as measured on the C3 dW
+// kernel) plus the fp32 partial planes the slices write and the optimiser kernel
+// reads back (8 bytes per element and slice at ~5 TB/s).  A count that just
+// overflows a round loses to one fewer slice: 72 tiles take 3 slices (216
+// workgroups, one round), not 4 (288, two rounds).
+uint32_t dw_dma_splits(uint32_t tiles, uint32_t Kp, uint64_t out_elems) {
+    constexpr uint32_t kCus = 256;
+    uint32_t best = 1;
+    double best_us = 0.0;
+    for (uint32_t req = 1; req <= 16 && (req == 1 || req <= Kp / 512); ++req) {
+        const uint32_t sp = gemm_dma_splits(Kp, req);
+        const uint32_t kps = ((Kp / req + 127) / 128) * 128;   // launch_gemm_dma's slice length
+        const uint32_t rounds = (tiles * sp + kCus - 1) / kCus;
+        const double us = rounds * (kps / 128.0) * 3.4 + (sp > 1 ? sp * (double)out_elems * 8.0 / 5.0e6 : 0.0);
+        if (req == 1 || us < best_us) {
+            best = sp;
+            best_us = us;
+        }
+    }
+    return best;
+}
+
 GemmPlan plan_gemm(const GemmLaunch &g) {
     GemmPlan p{};
     p.splits = 1;
@@ -167,14 +192,7 @@ GemmPlan plan_gemm(const GemmLaunch &g) {
     if (g.dtype == SKL_F16 && gemm_dma_enabled() && g.M && g.N && g.K) {
         const uint32_t Mp = round_up(g.M, 256), Np = round_up(g.N, 256), Kp = round_up(g.K, 128);
         const uint32_t tiles = (Mp / 256) * (Np / 256);
-        uint32_t splits = 1;
-        if (dw && tiles < 160) {
-            splits = (256 + tiles - 1) / tiles;
-            if (splits > Kp / 512) splits = Kp / 512;   // slices of at least 512 k
-            if (splits > 16) splits = 16;
-            if (splits < 1) splits = 1;
-            splits = gemm_dma_splits(Kp, splits);
-        }
+        const uint32_t splits = dw && tiles < 160 ? dw_dma_splits(tiles, Kp, (uint64_t)Mp * Np) : 1;
         const bool waste_ok = (uint64_t)Mp * Np <= (uint64_t)g.M * g.N * 3 / 2;
         // the kernel's operand offsets are 32-bit
         const uint64_t a_span = g.a_kcontig ? (uint64_t)Mp * (g.lda > Kp ? g.lda : Kp)

@@ -279,6 +279,132 @@ template <typename T, bool VEC, int PER> __global__ void __launch_bounds__(256) 
     }
 }
 
+// Rows that do not start on a 4-element boundary of their buffers (widths not a
+// multiple of 4): thread t owns the 4-element groups t, t + 256, ... of the buffer
+// that overlap the row, aligned in the buffer, so each tensor moves one 8-byte
+// (fp16) / 16-byte (fp32) access per group instead of four element accesses.  A
+// group that straddles the row's first or last element contributes only the row's
+// own elements to the statistics and is stored element by element, only those
+// elements (the neighbouring row's are another workgroup's).  A group holding a
+// valid element lies inside the buffer's aligned chunk of that element, so its
+// loads stay inside the allocation.  Needs every row tensor 4-element aligned.
+// PER = groups per thread: rows up to 1024 PER - 3 elements.  Per element the
+// arithmetic is that of norm_rows_reg_kernel.
+template <typename T, int PER> __global__ void __launch_bounds__(256) norm_rows_grp_kernel(RowNormArgs a) {
+    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+    typedef typename std::conditional<sizeof(T) == 2, u32x2_t, u32x4_t>::type G;   // 4 elements
+    __shared__ float red[4];
+    const uint32_t row = blockIdx.x;
+    const uint32_t n = a.n;
+    const uint64_t base = (uint64_t)row * n;
+    const uint32_t off = (uint32_t)(base & 3u);        // row start within its group
+    const uint64_t g0 = base >> 2;                     // group holding the row's first element
+    const uint32_t ng = (off + n + 3u) >> 2;           // groups overlapping the row
+    float z[PER][4];
+    bool has[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const uint32_t j = threadIdx.x + 256u * i;
+        has[i] = j < ng;
+        T v[4] = {(T)0, (T)0, (T)0, (T)0};
+        if (has[i]) *reinterpret_cast<G *>(v) = reinterpret_cast<const G *>(a.prenorm)[g0 + j];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int c = (int)(4u * j) + e - (int)off;    // column of element e
+            z[i][e] = (has[i] && c >= 0 && c < (int)n) ? to_f32(v[e]) : 0.0f;
+        }
+    }
+    float mean = 0.0f, rstd32;
+    T rstd_t;
+    if (a.norm == 1) {
+        float sq = 0.0f;
+#pragma unroll
+        for (int i = 0; i < PER; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sq = fmaf(z[i][e], z[i][e], sq);
+        sq = block_sum256(sq, red);
+        rstd32 = 1.0f / sqrtf(sq / (float)n + 1e-6f);
+        rstd_t = from_f32<T>(rstd32);
+    } else {
+        float sm = 0.0f;
+#pragma unroll
+        for (int i = 0; i < PER; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sm += z[i][e];
+        mean = block_sum256(sm, red) / (float)n;
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < PER; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int c = (int)(4u * (threadIdx.x + 256u * i)) + e - (int)off;
+                const float v = (has[i] && c >= 0 && c < (int)n) ? z[i][e] - mean : 0.0f;
+                ss = fmaf(v, v, ss);
+            }
+        ss = block_sum256(ss, red);
+        rstd32 = 1.0f / sqrtf(ss / (float)n + 1e-6f);
+        rstd_t = from_f32<T>(rstd32);
+    }
+    if (threadIdx.x == 0) stv<T>(a.norm_rstd, row, rstd_t);
+    const float scale = a.use_dropout ? 1.0f / (1.0f - a.p) : 1.0f;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        if (!has[i]) continue;
+        const uint32_t j = threadIdx.x + 256u * i;
+        const int c0 = (int)(4u * j) - (int)off;         // column of element 0 (may be < 0)
+        const bool whole = c0 >= 0 && c0 + 3 < (int)n;
+        T cen[4], pre[4], pd[4], mk[4], ot[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int c = c0 + e;
+            const bool ok = c >= 0 && c < (int)n;
+            const uint32_t cc = ok ? (uint32_t)c : 0u;
+            const float gw = ok ? to_f32(ldv<T>(a.norm_w, cc)) : 0.0f;
+            const float zv = z[i][e];
+            T p;
+            if (a.norm == 1) {
+                cen[e] = from_f32<T>(zv);
+                p = from_f32<T>(to_f32(from_f32<T>(zv * to_f32(rstd_t))) * gw);
+            } else {
+                const float gb = ok ? to_f32(ldv<T>(a.norm_b, cc)) : 0.0f;
+                const float v = zv - mean;
+                cen[e] = from_f32<T>(v);
+                p = from_f32<T>(fmaf(v * rstd32, gw, gb));
+            }
+            pre[e] = p;
+            const float act = activation(a.act, to_f32(p), a.leaky);
+            pd[e] = from_f32<T>(act);
+            if (a.use_dropout) {
+                const bool keep = dropout_u(cc, row, a.seed + row * 7u) >= a.p;
+                mk[e] = keep ? from_f32<T>(scale) : (T)0;
+                ot[e] = keep ? from_f32<T>(act * scale) : (T)0;
+            } else {
+                ot[e] = pd[e];
+            }
+        }
+        const uint64_t gi = g0 + j;
+        if (whole) {
+            reinterpret_cast<G *>(a.centered)[gi] = *reinterpret_cast<G *>(cen);
+            reinterpret_cast<G *>(a.preact)[gi] = *reinterpret_cast<G *>(pre);
+            reinterpret_cast<G *>(a.predrop)[gi] = *reinterpret_cast<G *>(pd);
+            reinterpret_cast<G *>(a.out)[gi] = *reinterpret_cast<G *>(ot);
+            if (a.use_dropout) reinterpret_cast<G *>(a.mask)[gi] = *reinterpret_cast<G *>(mk);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int c = c0 + e;
+                if (c < 0 || c >= (int)n) continue;
+                const uint64_t idx = base + (uint32_t)c;
+                stv<T>(a.centered, idx, cen[e]);
+                stv<T>(a.preact, idx, pre[e]);
+                stv<T>(a.predrop, idx, pd[e]);
+                stv<T>(a.out, idx, ot[e]);
+                if (a.use_dropout) stv<T>(a.mask, idx, mk[e]);
+            }
+        }
+    }
+}
+
 // BatchNorm: one thread per column over the batch rows (forward.cu:74-126 with
 // norm == 3), then act + dropout.  Consecutive threads read consecutive columns.
 template <typename T> __global__ void __launch_bounds__(256) norm_cols_kernel(RowNormArgs a) {
@@ -309,14 +435,31 @@ template <typename T> __global__ void __launch_bounds__(256) norm_cols_kernel(Ro
 
 static bool a16p(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Rows up to 256 x 16 elements run with the row in registers; longer rows take
-// the looping kernel.
+// Rows up to 256 x 16 elements run with the row in registers (16-byte chunks when
+// rows are 16-byte aligned, aligned 4-element groups when only the buffers are);
+// longer rows take the looping kernel.
 template <typename T> static void launch_norm_rows(const RowNormArgs &a, hipStream_t s) {
     constexpr uint32_t VW = 16 / sizeof(T);
     const bool vec = a.n % VW == 0 && a16p(a.prenorm) && a16p(a.norm_w) && (a.norm != 2 || a16p(a.norm_b)) &&
                      a16p(a.centered) && a16p(a.preact) && a16p(a.predrop) && a16p(a.out) &&
                      (!a.use_dropout || a16p(a.mask));
+    // 4-element groups aligned in every row tensor (rows that are not)
+    constexpr uintptr_t GB = 4 * sizeof(T) - 1;
+    auto ga = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & GB) == 0; };
+    const bool grp = ga(a.prenorm) && ga(a.centered) && ga(a.preact) && ga(a.predrop) && ga(a.out) &&
+                     (!a.use_dropout || ga(a.mask));
     const dim3 g(a.m), b(256);
+    if (!vec && grp && a.n <= 4 * 1024 - 3) {
+        if (a.n <= 1024 - 3)
+            hipLaunchKernelGGL((norm_rows_grp_kernel<T, 1>), g, b, 0, s, a);
+        else if (a.n <= 2 * 1024 - 3)
+            hipLaunchKernelGGL((norm_rows_grp_kernel<T, 2>), g, b, 0, s, a);
+        else if (a.n <= 3 * 1024 - 3)
+            hipLaunchKernelGGL((norm_rows_grp_kernel<T, 3>), g, b, 0, s, a);
+        else
+            hipLaunchKernelGGL((norm_rows_grp_kernel<T, 4>), g, b, 0, s, a);
+        return;
+    }
     if (vec && a.n <= 256 * VW)
         hipLaunchKernelGGL((norm_rows_reg_kernel<T, true, 1>), g, b, 0, s, a);
     else if (vec && a.n <= 2 * 256 * VW)
@@ -907,55 +1050,63 @@ hipError_t launch_dw_reduce_opt(const DwReduceArgs &a, hipStream_t s) {
 
 // ---- zero-padded fp16 copy (operand staging for the 256x256 GEMM) -----------------------
 // out[r][c] = (r < rows && c < cols) ? in[r ld + c] : 0 for r < rows_p, c < cols_p
-// (cols_p a multiple of 8): a thread writes 8 consecutive halves (16 bytes).
-// chunks (16-byte aligned source base): a source window that is not 16-byte
-// aligned is cut out of the two aligned 16-byte chunks covering it (funnel
-// shifts), as long as both lie inside the source's readable elements; element
-// loads otherwise.
+// (cols_p a multiple of 8).  One wave per padded row (grid-stride over rows), lane
+// l writing the 16-byte chunks l, l + 64, ... of it; 32-bit index arithmetic only.
+// Every chunk of a row starts (r ld) mod 8 elements past a 16-byte boundary of the
+// source, so with a 16-byte aligned base (chunks) a chunk is cut out of the two
+// aligned 16-byte source chunks covering it (funnel shifts by that row-wide
+// amount), as long as both lie inside the source's readable elements; element
+// loads otherwise (the row's last partial chunk, the buffer's tail).
 __global__ void __launch_bounds__(256) pad_h_kernel(const half_t *__restrict__ in, uint32_t rows, uint32_t cols,
                                                     uint32_t ld, half_t *__restrict__ out, uint32_t rows_p,
                                                     uint32_t cols_p, uint32_t chunks) {
     const uint32_t gpr = cols_p / 8;
-    const uint64_t total = (uint64_t)rows_p * gpr;
     const uint64_t in_elems = rows ? (uint64_t)(rows - 1) * ld + cols : 0;   // readable source elements
-    for (uint64_t q = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; q < total;
-         q += (uint64_t)gridDim.x * blockDim.x) {
-        const uint32_t r = (uint32_t)(q / gpr), c = (uint32_t)(q % gpr) * 8;
-        u32x4_t v = {0, 0, 0, 0};
-        if (r < rows && c < cols) {
-            const uint64_t e0 = (uint64_t)r * ld + c;            // first source element
-            const uint64_t a0 = e0 & ~(uint64_t)7;                // its aligned chunk
-            const uint32_t sh = (uint32_t)(e0 - a0) * 2;           // byte offset within it
-            if (chunks && c + 8 <= cols && a0 + (sh ? 16 : 8) <= in_elems) {
-                const u32x4_t lo = *reinterpret_cast<const u32x4_t *>(in + a0);
-                const u32x4_t hi = sh ? *reinterpret_cast<const u32x4_t *>(in + a0 + 8) : lo;
-                const uint32_t w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-                const uint32_t wd = sh >> 2, bits = (sh & 3u) * 8u;   // whole dwords, then 0 or 16 bits
-#pragma unroll
-                for (int d = 0; d < 4; ++d) {
-                    const uint32_t x0 = wd == 0 ? w[d] : wd == 1 ? w[d + 1] : wd == 2 ? w[d + 2] : w[d + 3];
-                    const uint32_t x1 = wd == 0 ? w[d + 1] : wd == 1 ? w[d + 2] : wd == 2 ? w[d + 3] : w[d + 4];
-                    v[d] = __builtin_amdgcn_alignbit(x1, x0, bits);   // (x1:x0) >> bits
-                }
-            } else {
-                half_t h[8];
-                const half_t *src = in + e0;
-#pragma unroll
-                for (uint32_t e = 0; e < 8; ++e) h[e] = c + e < cols ? src[e] : (half_t)0;
-                v = __builtin_bit_cast(u32x4_t, h);
-            }
+    const uint32_t lane = threadIdx.x & 63u;
+    for (uint32_t r = blockIdx.x * 4u + (threadIdx.x >> 6); r < rows_p; r += gridDim.x * 4u) {
+        u32x4_t *orow = reinterpret_cast<u32x4_t *>(out + (uint64_t)r * cols_p);
+        if (r >= rows) {
+            for (uint32_t g = lane; g < gpr; g += 64u) orow[g] = u32x4_t{0, 0, 0, 0};
+            continue;
         }
-        *reinterpret_cast<u32x4_t *>(out + (uint64_t)r * cols_p + c) = v;
+        const uint64_t rb = (uint64_t)r * ld;                   // first source element of the row
+        const uint32_t sh = (uint32_t)(rb & 7u) * 2u;           // its byte offset within an aligned chunk
+        const half_t *abase = in + (rb - (rb & 7u));            // aligned chunk holding it
+        const uint32_t wd = sh >> 2, bits = (sh & 3u) * 8u;     // whole dwords, then 0 or 16 bits
+        for (uint32_t g = lane; g < gpr; g += 64u) {
+            const uint32_t c = g * 8u;
+            u32x4_t v = {0, 0, 0, 0};
+            if (c < cols) {
+                if (chunks && c + 8u <= cols && rb - (rb & 7u) + c + (sh ? 16u : 8u) <= in_elems) {
+                    const u32x4_t lo = *reinterpret_cast<const u32x4_t *>(abase + c);
+                    const u32x4_t hi = sh ? *reinterpret_cast<const u32x4_t *>(abase + c + 8u) : lo;
+                    const uint32_t w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) {
+                        const uint32_t x0 = wd == 0 ? w[d] : wd == 1 ? w[d + 1] : wd == 2 ? w[d + 2] : w[d + 3];
+                        const uint32_t x1 = wd == 0 ? w[d + 1] : wd == 1 ? w[d + 2] : wd == 2 ? w[d + 3] : w[d + 4];
+                        v[d] = __builtin_amdgcn_alignbit(x1, x0, bits);   // (x1:x0) >> bits
+                    }
+                } else {
+                    half_t h[8];
+                    const half_t *src = in + rb + c;
+#pragma unroll
+                    for (uint32_t e = 0; e < 8; ++e) h[e] = c + e < cols ? src[e] : (half_t)0;
+                    v = __builtin_bit_cast(u32x4_t, h);
+                }
+            }
+            orow[g] = v;
+        }
     }
 }
 
 hipError_t launch_pad_h(const void *in, uint32_t rows, uint32_t cols, uint32_t ld, void *out, uint32_t rows_p,
                         uint32_t cols_p, hipStream_t s) {
     if (cols_p % 8 || rows_p < rows || cols_p < cols || !a16(out)) return hipErrorInvalidValue;
-    const uint64_t groups = (uint64_t)rows_p * (cols_p / 8);
-    if (groups == 0) return hipSuccess;
-    hipLaunchKernelGGL(pad_h_kernel, grid_for(groups, 256), dim3(256), 0, s, reinterpret_cast<const half_t *>(in),
-                       rows, cols, ld, reinterpret_cast<half_t *>(out), rows_p, cols_p, a16(in) ? 1u : 0u);
+    if (rows_p == 0 || cols_p == 0) return hipSuccess;
+    const uint32_t blocks = (rows_p + 3) / 4 < 8192 ? (rows_p + 3) / 4 : 8192;   // 4 rows per block
+    hipLaunchKernelGGL(pad_h_kernel, dim3(blocks), dim3(256), 0, s, reinterpret_cast<const half_t *>(in), rows,
+                       cols, ld, reinterpret_cast<half_t *>(out), rows_p, cols_p, a16(in) ? 1u : 0u);
     return hipGetLastError();
 }
 

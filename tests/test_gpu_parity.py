@@ -62,6 +62,12 @@ FWD_CASES = [
     (96, 80, 144, 2, 3, 0.2),       # LayerNorm + LeakyReLU + dropout
     (64, 48, 40, 3, 4, 0.0),        # BatchNorm + Tanh
     (33, 17, 11, 2, 1, 0.0),        # LN + Sigmoid, ragged
+    # widths that are not a multiple of 4: rows start at every offset within
+    # a 4-element group (the aligned-group norm kernel, 1..4 groups per thread)
+    (301, 64, 1531, 2, 3, 0.1),     # LN + LeakyReLU + dropout
+    (130, 40, 3001, 1, 7, 0.0),     # RMSNorm + Mish
+    (70, 32, 1022, 2, 6, 0.0),      # LN + SiLU, width 2 mod 4
+    (50, 24, 4093, 1, 4, 0.2),      # RMSNorm + Tanh + dropout, 4 groups per thread
 ]
 
 

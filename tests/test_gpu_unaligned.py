@@ -1,4 +1,4 @@
-"""Parity of the error kernels on rows that do not start on a 4-element boundary:
+"""Parity of the error and norm kernels on rows that do not start on a 4-element boundary:
 an odd output width (every row at a different offset) and buffers whose base
 pointers sit 1..3 elements past a 16-byte boundary (torch views into a larger
 allocation).  These take the 4-column-group path that reads aligned chunks and
@@ -99,3 +99,30 @@ def test_output_error_odd_width(ctx, half):
     tol = FP16_TOL if half else FP32_TOL
     for n in ("grad", "d_prenorm", "d_norm_w", "d_norm_b"):
         check(n, db.get(n), getattr(ob, n), tol)
+
+
+FWD_CACHES = ("z", "prenorm", "centered", "preact", "predrop", "out", "mask")
+
+
+@pytest.mark.parametrize("off", [1, 4])
+@pytest.mark.parametrize("norm", [1, 2])
+def test_forward_norm_misaligned_buffers(ctx, norm, off):
+    """The row-norm forward on fp16 caches starting `off` elements past an aligned
+    allocation: 4 elements keeps 8-byte groups aligned (aligned-group kernel), 1 does
+    not (element kernel)."""
+    M, K, N = 203, 48, 1024
+    ob, db = make_pair(ctx, K, N, M, seed=81 + off, half=True, norm=norm, act=abi.ACT_SILU, p=0.1)
+    for name in FWD_CACHES:
+        t = getattr(db, name, None)
+        if t is None:
+            continue
+        buf = torch.zeros(t.numel() + 8, device=t.device, dtype=t.dtype)
+        setattr(db, name, buf[off:off + t.numel()].view(t.shape))
+    x = inputs(82, M, K, True)
+    seed = O.scramble_seed(5, 9)
+    print(f"forward norm={norm} offset={off}", flush=True)
+    ob.forward(x, M, True, seed)
+    db.forward(dev(x, True), M, True, seed)
+    torch.cuda.synchronize()
+    for n in ("preact", "predrop", "out", "mask", "centered"):
+        check(n, db.get(n), getattr(ob, n), FP16_TOL)

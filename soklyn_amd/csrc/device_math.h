@@ -111,6 +111,11 @@ __device__ __forceinline__ float activation_derivative(uint32_t act, float err, 
     }
 }
 
+// Which operands activation_derivative reads: the activation's output (out_v)
+// or its input (in_x).
+__host__ __device__ __forceinline__ bool act_uses_output(uint32_t act) { return (act >= 1 && act <= 4) || act == 6; }
+__host__ __device__ __forceinline__ bool act_uses_input(uint32_t act) { return act == 6 || act == 7; }
+
 // math.cuh:45-53.  The 64-bit product col * 6364136223846793005 keeps only its
 // low 32 bits in the 32-bit state, i.e. col * 0x4C957F2D mod 2^32.
 __device__ __forceinline__ float dropout_u(uint32_t col, uint32_t row, uint32_t seed) {

@@ -894,8 +894,16 @@ hipError_t launch_output_error(const ErrArgs &a, float *partials, uint32_t split
     return hipGetLastError();
 }
 
-hipError_t launch_error_from_sum(const ErrArgs &a, float *partials, uint32_t splits, hipStream_t s) {
-    if ((uint64_t)a.rows * a.n == 0) return hipSuccess;
+hipError_t launch_error_from_sum(const ErrArgs &a0, float *partials, uint32_t splits, hipStream_t s) {
+    if ((uint64_t)a0.rows * a0.n == 0) return hipSuccess;
+    // activation_derivative reads the output (predrop) for sigmoid, ReLU, leaky
+    // ReLU, tanh and SiLU, the input (preact) for SiLU and Mish.  An operand it
+    // does not read aliases the mask (same element type and index, loaded
+    // anyway), so its loads hit in cache instead of streaming another [rows x n]
+    // tensor from HBM, and the kernel keeps its batched loads free of branches.
+    ErrArgs a = a0;
+    if (!act_uses_output(a.act)) a.predrop = a.mask;
+    if (!act_uses_input(a.act)) a.preact = a.mask;
     if (a.dtype == 1)
         launch_error_t<true, half_t>(a, partials, splits, s);
     else

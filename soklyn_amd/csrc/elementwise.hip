@@ -1027,32 +1027,73 @@ hipError_t launch_vec_opt(const VecOptArgs &a, hipStream_t s) {
 }
 
 // ---- split-K dW reduction + W optimiser ----------------------------------------------
-template <typename T> __global__ void dw_reduce_opt_kernel(DwReduceArgs a) {
-    const uint64_t total = (uint64_t)a.rows * a.n;
-    for (uint64_t idx = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
-         idx += (uint64_t)gridDim.x * blockDim.x) {
-        const uint64_t r = idx / a.n, c = idx - r * a.n;
-        const float *pp = a.partials + r * a.pld + c;
-        float s = 0.0f;
-        for (uint32_t sp = 0; sp < a.splits; ++sp) s += pp[(uint64_t)sp * a.plane];
-        const OptEpi &e = a.e;
-        float p = e.master[idx], v = e.dv[idx], mm = e.dm[idx];
-        optimiser_step(p, v, mm, s * kLossScaleInv, e.inv_m, e.lr, e.clamp, e.opt, e.regularisation, e.regu_coeff,
-                       true);
-        e.master[idx] = p;
-        e.dv[idx] = v;
-        e.dm[idx] = mm;
-        if (e.param) stv<T>(e.param, idx, from_f32<T>(p));
+// Thread (x, y) owns VW consecutive columns c of the rows y, y + gridDim.y, ...: it
+// adds the partial planes in split order (8 loads in flight; the same sequence of
+// additions as one load at a time), then applies the optimiser to each element.
+// VW = 4 (16-byte accesses) when n, the plane pitches and every buffer allow it.
+template <typename T, int VW> __global__ void __launch_bounds__(256) dw_reduce_opt_kernel(DwReduceArgs a) {
+    const uint32_t c = (blockIdx.x * 256u + threadIdx.x) * VW;
+    if (c >= a.n) return;
+    const OptEpi &e = a.e;
+    typedef typename std::conditional<VW == 4, f32x4, float>::type V;
+    for (uint32_t r = blockIdx.y; r < a.rows; r += gridDim.y) {
+        const float *pp = a.partials + (uint64_t)r * a.pld + c;
+        V sum = V{};
+        uint32_t sp = 0;
+        for (; sp + 8 <= a.splits; sp += 8) {
+            V v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = *reinterpret_cast<const V *>(pp + (uint64_t)(sp + i) * a.plane);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) sum += v[i];
+        }
+        for (; sp < a.splits; ++sp) sum += *reinterpret_cast<const V *>(pp + (uint64_t)sp * a.plane);
+        const uint64_t idx = (uint64_t)r * a.n + c;
+        V p = *reinterpret_cast<const V *>(e.master + idx), dv = *reinterpret_cast<const V *>(e.dv + idx),
+          dm = *reinterpret_cast<const V *>(e.dm + idx);
+        if constexpr (VW == 4) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float pj = p[j], vj = dv[j], mj = dm[j];
+                optimiser_step(pj, vj, mj, sum[j] * kLossScaleInv, e.inv_m, e.lr, e.clamp, e.opt, e.regularisation,
+                               e.regu_coeff, true);
+                p[j] = pj;
+                dv[j] = vj;
+                dm[j] = mj;
+            }
+            if (e.param) store4<T>(e.param, idx, p);
+        } else {
+            optimiser_step(p, dv, dm, sum * kLossScaleInv, e.inv_m, e.lr, e.clamp, e.opt, e.regularisation,
+                           e.regu_coeff, true);
+            if (e.param) stv<T>(e.param, idx, from_f32<T>(p));
+        }
+        *reinterpret_cast<V *>(e.master + idx) = p;
+        *reinterpret_cast<V *>(e.dv + idx) = dv;
+        *reinterpret_cast<V *>(e.dm + idx) = dm;
     }
 }
 
-hipError_t launch_dw_reduce_opt(const DwReduceArgs &a, hipStream_t s) {
-    const uint64_t total = (uint64_t)a.rows * a.n;
-    if (total == 0) return hipSuccess;
-    if (a.dtype == 1)
-        hipLaunchKernelGGL(dw_reduce_opt_kernel<half_t>, grid_for(total, 256), dim3(256), 0, s, a);
+static bool aligned_to(const void *p, uintptr_t b) { return (reinterpret_cast<uintptr_t>(p) & (b - 1)) == 0; }
+
+template <typename T> static void launch_dw_reduce_t(const DwReduceArgs &a, hipStream_t s) {
+    const bool vec = a.n % 4 == 0 && a.pld % 4 == 0 && a.plane % 4 == 0 && aligned_to(a.partials, 16) &&
+                     aligned_to(a.e.master, 16) && aligned_to(a.e.dv, 16) && aligned_to(a.e.dm, 16) &&
+                     (!a.e.param || aligned_to(a.e.param, 4 * sizeof(T)));
+    const uint32_t vw = vec ? 4u : 1u;
+    const uint32_t gx = cdiv(a.n, 256u * vw);
+    const uint32_t gy = a.rows < cdiv(4096, gx) ? a.rows : cdiv(4096, gx);   // ~4096 workgroups
+    if (vec)
+        hipLaunchKernelGGL((dw_reduce_opt_kernel<T, 4>), dim3(gx, gy), dim3(256), 0, s, a);
     else
-        hipLaunchKernelGGL(dw_reduce_opt_kernel<float>, grid_for(total, 256), dim3(256), 0, s, a);
+        hipLaunchKernelGGL((dw_reduce_opt_kernel<T, 1>), dim3(gx, gy), dim3(256), 0, s, a);
+}
+
+hipError_t launch_dw_reduce_opt(const DwReduceArgs &a, hipStream_t s) {
+    if ((uint64_t)a.rows * a.n == 0) return hipSuccess;
+    if (a.dtype == 1)
+        launch_dw_reduce_t<half_t>(a, s);
+    else
+        launch_dw_reduce_t<float>(a, s);
     return hipGetLastError();
 }
 

@@ -258,7 +258,11 @@ hipError_t timed_gemm(skl_ctx *ctx, const GemmLaunch &g0, GemmKind kind, float *
 // Runs g as planned; ws holds plan.bytes() of workspace.  full_out: the output
 // buffer has room for the padded grid (p.Mp x p.Np at its ldc), so the kernel
 // may write all of it (rows and columns past M, N come out zero).
-int32_t exec_gemm(skl_ctx *ctx, GemmLaunch g, const GemmPlan &p, char *ws, bool full_out = false) {
+// vec (a dW only): the bias / norm-parameter update to run inside the split-K
+// reduction's launch when there is one; *vec_done says whether it ran.
+int32_t exec_gemm(skl_ctx *ctx, GemmLaunch g, const GemmPlan &p, char *ws, bool full_out = false,
+                  const VecOptArgs *vec = nullptr, bool *vec_done = nullptr) {
+    if (vec_done) *vec_done = false;
     char *wa = ws, *wb = ws + p.a_bytes, *wpart = ws + p.a_bytes + p.b_bytes;
     const OptEpi oe = g.opt;
     const uint32_t M = g.M, N = g.N;
@@ -274,7 +278,12 @@ int32_t exec_gemm(skl_ctx *ctx, GemmLaunch g, const GemmPlan &p, char *ws, bool 
         d.plane = (uint64_t)M * 16;
         d.pld = 16;
         d.e = oe;
+        if (vec) {
+            d.with_vec = 1;
+            d.vec = *vec;
+        }
         SKL_TRY(launch_dw_reduce_opt(d, ctx->stream));
+        if (vec_done) *vec_done = vec != nullptr;
         return SKL_OK;
     }
     if (p.dma) {
@@ -330,7 +339,12 @@ int32_t exec_gemm(skl_ctx *ctx, GemmLaunch g, const GemmPlan &p, char *ws, bool 
         d.plane = p.dma ? (uint64_t)p.Mp * p.Np : (uint64_t)M * N;
         d.pld = p.dma ? p.Np : N;
         d.e = oe;
+        if (vec) {
+            d.with_vec = 1;
+            d.vec = *vec;
+        }
         SKL_TRY(launch_dw_reduce_opt(d, ctx->stream));
+        if (vec_done) *vec_done = vec != nullptr;
     }
     return SKL_OK;
 }
@@ -838,7 +852,6 @@ static int32_t backward_impl(skl_ctx *ctx, const skl_dense_desc *b, const void *
     if ((r = ensure_ws(ctx, gemm_bytes + col_bytes))) return r;
     char *ws = reinterpret_cast<char *>(ctx->ws);
     float *ws_col = reinterpret_cast<float *>(ws + gemm_bytes);
-    if ((r = exec_gemm(ctx, g, plan, ws))) return r;
 
     // -- db, sum dNorm_w, sum dNorm_b and their optimiser steps -----------------------
     VecOptArgs v{};
@@ -865,10 +878,13 @@ static int32_t backward_impl(skl_ctx *ctx, const skl_dense_desc *b, const void *
     v.lr = t->learn_rate;
     v.clamp = t->grad_clamp;
     v.inv_m = inv_m;
-    if (v.enabled[0] || v.enabled[1] || v.enabled[2]) {
-        if (!cached) SKL_TRY(launch_colsum(v, ctx->stream));
-        SKL_TRY(launch_vec_opt(v, ctx->stream));
-    }
+    const bool any_vec = v.enabled[0] || v.enabled[1] || v.enabled[2];
+    // the column sums read only the error call's outputs, so they go first; the
+    // parameter update then rides in the dW's split-K reduction launch when it has one
+    if (any_vec && !cached) SKL_TRY(launch_colsum(v, ctx->stream));
+    bool vec_done = false;
+    if ((r = exec_gemm(ctx, g, plan, ws, false, any_vec ? &v : nullptr, &vec_done))) return r;
+    if (any_vec && !vec_done) SKL_TRY(launch_vec_opt(v, ctx->stream));
     return SKL_OK;
 }
 

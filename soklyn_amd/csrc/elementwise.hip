@@ -930,10 +930,10 @@ __global__ void __launch_bounds__(256) colsum_kernel(VecOptArgs a) {
 // 16 columns per workgroup, 16 lanes per column: lane j sums the partials of
 // splits j, j+16, ... in order (four loads in flight per batch), then the 16
 // are added in a fixed pairwise order.
-template <typename T> __global__ void __launch_bounds__(256) vec_opt_kernel(VecOptArgs a) {
+template <typename T> __device__ __forceinline__ void vec_opt_block(const VecOptArgs &a, uint32_t block) {
     __shared__ float red[3][16][17];
     const uint32_t cl = threadIdx.x & 15u, j = threadIdx.x >> 4;
-    const uint32_t col = blockIdx.x * 16 + cl;
+    const uint32_t col = block * 16 + cl;
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
         float s = 0.0f;
@@ -969,6 +969,7 @@ template <typename T> __global__ void __launch_bounds__(256) vec_opt_kernel(VecO
         if (a.param[k]) stv<T>(a.param[k], col, from_f32<T>(p));
     }
 }
+template <typename T> __global__ void __launch_bounds__(256) vec_opt_kernel(VecOptArgs a) { vec_opt_block<T>(a, blockIdx.x); }
 
 // Vector column sums: a thread owns 4 consecutive columns (one 16-byte load per
 // row); the row range of its split is walked 8 rows at a time for loads in flight.
@@ -1031,12 +1032,21 @@ hipError_t launch_vec_opt(const VecOptArgs &a, hipStream_t s) {
 // adds the partial planes in split order (8 loads in flight; the same sequence of
 // additions as one load at a time), then applies the optimiser to each element.
 // VW = 4 (16-byte accesses) when n, the plane pitches and every buffer allow it.
-template <typename T, int VW> __global__ void __launch_bounds__(256) dw_reduce_opt_kernel(DwReduceArgs a) {
-    const uint32_t c = (blockIdx.x * 256u + threadIdx.x) * VW;
+// Grid: 1-D, blocks [0, a.vec_blocks) run the bias / norm-parameter update of
+// a.vec (vec_opt_block; independent of W), the next gx * gy blocks the reduction
+// (block gx * y + x).
+template <typename T, int VW> __global__ void __launch_bounds__(256) dw_reduce_opt_kernel(DwReduceArgs a, uint32_t gx,
+                                                                                         uint32_t gy) {
+    if (blockIdx.x < a.vec_blocks) {
+        vec_opt_block<T>(a.vec, blockIdx.x);
+        return;
+    }
+    const uint32_t bid = blockIdx.x - a.vec_blocks, bx = bid % gx, by = bid / gx;
+    const uint32_t c = (bx * 256u + threadIdx.x) * VW;
     if (c >= a.n) return;
     const OptEpi &e = a.e;
     typedef typename std::conditional<VW == 4, f32x4, float>::type V;
-    for (uint32_t r = blockIdx.y; r < a.rows; r += gridDim.y) {
+    for (uint32_t r = by; r < a.rows; r += gy) {
         const float *pp = a.partials + (uint64_t)r * a.pld + c;
         V sum = V{};
         uint32_t sp = 0;
@@ -1082,14 +1092,17 @@ template <typename T> static void launch_dw_reduce_t(const DwReduceArgs &a, hipS
     const uint32_t vw = vec ? 4u : 1u;
     const uint32_t gx = cdiv(a.n, 256u * vw);
     const uint32_t gy = a.rows < cdiv(4096, gx) ? a.rows : cdiv(4096, gx);   // ~4096 workgroups
+    const dim3 grid(a.vec_blocks + gx * gy);
     if (vec)
-        hipLaunchKernelGGL((dw_reduce_opt_kernel<T, 4>), dim3(gx, gy), dim3(256), 0, s, a);
+        hipLaunchKernelGGL((dw_reduce_opt_kernel<T, 4>), grid, dim3(256), 0, s, a, gx, gy);
     else
-        hipLaunchKernelGGL((dw_reduce_opt_kernel<T, 1>), dim3(gx, gy), dim3(256), 0, s, a);
+        hipLaunchKernelGGL((dw_reduce_opt_kernel<T, 1>), grid, dim3(256), 0, s, a, gx, gy);
 }
 
-hipError_t launch_dw_reduce_opt(const DwReduceArgs &a, hipStream_t s) {
-    if ((uint64_t)a.rows * a.n == 0) return hipSuccess;
+hipError_t launch_dw_reduce_opt(const DwReduceArgs &a0, hipStream_t s) {
+    DwReduceArgs a = a0;
+    a.vec_blocks = a.with_vec && a.vec.n ? cdiv(a.vec.n, 16) : 0;
+    if ((uint64_t)a.rows * a.n == 0) return a.vec_blocks ? launch_vec_opt(a.vec, s) : hipSuccess;
     if (a.dtype == 1)
         launch_dw_reduce_t<half_t>(a, s);
     else

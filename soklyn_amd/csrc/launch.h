@@ -144,6 +144,10 @@ struct DwReduceArgs {
     uint64_t plane;
     uint32_t pld, pad;
     OptEpi e;
+    // with_vec: the same launch also runs launch_vec_opt(vec) (the bias / norm-
+    // parameter update, independent of W) in its first workgroups
+    uint32_t with_vec, vec_blocks;
+    VecOptArgs vec;
 };
 hipError_t launch_dw_reduce_opt(const DwReduceArgs &a, hipStream_t s);
 

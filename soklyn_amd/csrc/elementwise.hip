@@ -927,13 +927,15 @@ __global__ void __launch_bounds__(256) colsum_kernel(VecOptArgs a) {
     }
 }
 
-// 16 columns per workgroup, 16 lanes per column: lane j sums the partials of
-// splits j, j+16, ... in order (four loads in flight per batch), then the 16
-// are added in a fixed pairwise order.
+// a.cpb columns per workgroup (a power of 2), 256 / cpb lanes per column: lane j
+// sums the partials of splits j, j + lanes, ... in order (8 loads in flight), then
+// the lanes of a column are added in a fixed tree (halving strides).  cpb comes
+// from vec_opt_cpb: about 8 splits per lane.
 template <typename T> __device__ __forceinline__ void vec_opt_block(const VecOptArgs &a, uint32_t block) {
-    __shared__ float red[3][16][17];
-    const uint32_t cl = threadIdx.x & 15u, j = threadIdx.x >> 4;
-    const uint32_t col = block * 16 + cl;
+    __shared__ float red[3][256];
+    const uint32_t cpb = a.cpb, lanes = 256u / cpb;
+    const uint32_t cl = threadIdx.x & (cpb - 1u), j = threadIdx.x / cpb;
+    const uint32_t col = block * cpb + cl;
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
         float s = 0.0f;
@@ -941,26 +943,30 @@ template <typename T> __device__ __forceinline__ void vec_opt_block(const VecOpt
             const float *p = a.partials + (uint64_t)k * a.n + col;
             const uint64_t st = (uint64_t)3 * a.n;   // between splits
             uint32_t sp = j;
-            for (; sp + 48 < a.splits; sp += 64) {
-                const float v0 = p[sp * st], v1 = p[(sp + 16) * st], v2 = p[(sp + 32) * st], v3 = p[(sp + 48) * st];
-                s += v0;
-                s += v1;
-                s += v2;
-                s += v3;
+            for (; sp + 7u * lanes < a.splits; sp += 8u * lanes) {
+                float v[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) v[u] = p[(uint64_t)(sp + u * lanes) * st];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) s += v[u];
             }
-            for (; sp < a.splits; sp += 16) s += p[sp * st];
+            for (; sp < a.splits; sp += lanes) s += p[(uint64_t)sp * st];
         }
-        red[k][j][cl] = s;
+        red[k][threadIdx.x] = s;   // = red[k][j cpb + cl]
     }
     __syncthreads();
+    for (uint32_t h = lanes / 2u; h >= 1u; h /= 2u) {
+        if (j < h) {
+#pragma unroll
+            for (int k = 0; k < 3; ++k) red[k][threadIdx.x] += red[k][threadIdx.x + h * cpb];
+        }
+        __syncthreads();
+    }
     if (j != 0 || col >= a.n) return;
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
         if (!a.enabled[k]) continue;
-        float t[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) t[i] = red[k][2 * i][cl] + red[k][2 * i + 1][cl];
-        const float s = ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
+        const float s = red[k][cl];
         float p = a.master[k][col], v = a.dv[k][col], mm = a.dm[k][col];
         optimiser_step(p, v, mm, s * kLossScaleInv, a.inv_m, a.lr, a.clamp, a.opt[k], 0, 0.0f, false);
         a.master[k][col] = p;
@@ -1018,12 +1024,22 @@ uint32_t colsum_splits(uint32_t rows, uint32_t n) {
     return sp < 1 ? 1 : sp;
 }
 
-hipError_t launch_vec_opt(const VecOptArgs &a, hipStream_t s) {
-    if (a.n == 0) return hipSuccess;
+// Columns per workgroup of the parameter update: lanes per column doubled from 16
+// (up to 256) until a lane has at most 8 of the `splits` partial rows to add.
+uint32_t vec_opt_cpb(uint32_t splits) {
+    uint32_t lanes = 16;
+    while (lanes < 256 && lanes * 8 < splits) lanes *= 2;
+    return 256 / lanes;
+}
+
+hipError_t launch_vec_opt(const VecOptArgs &a0, hipStream_t s) {
+    if (a0.n == 0) return hipSuccess;
+    VecOptArgs a = a0;
+    a.cpb = vec_opt_cpb(a.splits);
     if (a.dtype == 1)
-        hipLaunchKernelGGL(vec_opt_kernel<half_t>, dim3(cdiv(a.n, 16)), dim3(256), 0, s, a);
+        hipLaunchKernelGGL(vec_opt_kernel<half_t>, dim3(cdiv(a.n, a.cpb)), dim3(256), 0, s, a);
     else
-        hipLaunchKernelGGL(vec_opt_kernel<float>, dim3(cdiv(a.n, 16)), dim3(256), 0, s, a);
+        hipLaunchKernelGGL(vec_opt_kernel<float>, dim3(cdiv(a.n, a.cpb)), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
@@ -1033,20 +1049,33 @@ hipError_t launch_vec_opt(const VecOptArgs &a, hipStream_t s) {
 // additions as one load at a time), then applies the optimiser to each element.
 // VW = 4 (16-byte accesses) when n, the plane pitches and every buffer allow it.
 // Grid: 1-D, blocks [0, a.vec_blocks) run the bias / norm-parameter update of
-// a.vec (vec_opt_block; independent of W), the next gx * gy blocks the reduction
-// (block gx * y + x).
+// a.vec (vec_opt_block; independent of W), the next blocks the reduction: block
+// gx * y + x, or for narrow outputs (gx = 0) one thread per element of the gy.
 template <typename T, int VW> __global__ void __launch_bounds__(256) dw_reduce_opt_kernel(DwReduceArgs a, uint32_t gx,
                                                                                          uint32_t gy) {
     if (blockIdx.x < a.vec_blocks) {
         vec_opt_block<T>(a.vec, blockIdx.x);
         return;
     }
-    const uint32_t bid = blockIdx.x - a.vec_blocks, bx = bid % gx, by = bid / gx;
-    const uint32_t c = (bx * 256u + threadIdx.x) * VW;
+    const uint32_t bid = blockIdx.x - a.vec_blocks;
+    uint32_t c, r0, rstep;
+    if (gx == 0) {
+        // narrow outputs (one element per thread, gy = elements): flat index
+        const uint32_t el = bid * 256u + threadIdx.x;
+        if (el >= gy) return;
+        r0 = el / a.n;
+        c = el - r0 * a.n;
+        rstep = a.rows;   // one row
+    } else {
+        const uint32_t bx = bid % gx;
+        r0 = bid / gx;
+        c = (bx * 256u + threadIdx.x) * VW;
+        rstep = gy;
+    }
     if (c >= a.n) return;
     const OptEpi &e = a.e;
     typedef typename std::conditional<VW == 4, f32x4, float>::type V;
-    for (uint32_t r = by; r < a.rows; r += gy) {
+    for (uint32_t r = r0; r < a.rows; r += rstep) {
         const float *pp = a.partials + (uint64_t)r * a.pld + c;
         V sum = V{};
         uint32_t sp = 0;
@@ -1090,6 +1119,13 @@ template <typename T> static void launch_dw_reduce_t(const DwReduceArgs &a, hipS
                      aligned_to(a.e.master, 16) && aligned_to(a.e.dv, 16) && aligned_to(a.e.dm, 16) &&
                      (!a.e.param || aligned_to(a.e.param, 4 * sizeof(T)));
     const uint32_t vw = vec ? 4u : 1u;
+    if (!vec && a.n < 128 && (uint64_t)a.rows * a.n < (1ull << 31)) {
+        // narrow: one thread per element (gx = 0 selects the flat index)
+        const uint32_t elems = a.rows * a.n;
+        hipLaunchKernelGGL((dw_reduce_opt_kernel<T, 1>), dim3(a.vec_blocks + cdiv(elems, 256)), dim3(256), 0, s, a,
+                           0u, elems);
+        return;
+    }
     const uint32_t gx = cdiv(a.n, 256u * vw);
     const uint32_t gy = a.rows < cdiv(4096, gx) ? a.rows : cdiv(4096, gx);   // ~4096 workgroups
     const dim3 grid(a.vec_blocks + gx * gy);
@@ -1101,7 +1137,8 @@ template <typename T> static void launch_dw_reduce_t(const DwReduceArgs &a, hipS
 
 hipError_t launch_dw_reduce_opt(const DwReduceArgs &a0, hipStream_t s) {
     DwReduceArgs a = a0;
-    a.vec_blocks = a.with_vec && a.vec.n ? cdiv(a.vec.n, 16) : 0;
+    a.vec.cpb = vec_opt_cpb(a.vec.splits);
+    a.vec_blocks = a.with_vec && a.vec.n ? cdiv(a.vec.n, a.vec.cpb) : 0;
     if ((uint64_t)a.rows * a.n == 0) return a.vec_blocks ? launch_vec_opt(a.vec, s) : hipSuccess;
     if (a.dtype == 1)
         launch_dw_reduce_t<half_t>(a, s);

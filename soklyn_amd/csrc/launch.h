@@ -131,8 +131,11 @@ struct VecOptArgs {
     uint32_t enabled[3];
     OptParams opt[3];
     float lr, clamp, inv_m;
+    uint32_t cpb;                 // columns per workgroup (set by the launchers)
 };
 hipError_t launch_colsum(const VecOptArgs &a, hipStream_t s);
+// Columns per workgroup of the parameter update for `splits` partial rows.
+uint32_t vec_opt_cpb(uint32_t splits);
 // Row splits for launch_colsum so the grid has ~1024 workgroups.
 uint32_t colsum_splits(uint32_t rows, uint32_t n);
 hipError_t launch_vec_opt(const VecOptArgs &a, hipStream_t s);

@@ -75,6 +75,34 @@ template <typename T> struct EpiFwdK {
             store4_nt<T>(e.out, idx, a);
         }
     }
+    // one element (ragged tiles): per-column operands loaded once per column
+    struct Col1 { float bias; };
+    __device__ __forceinline__ static Col1 column1(const FwdEpi &e, uint32_t n) {
+        return Col1{e.bias ? to_f32(ld_t<T>(e.bias, n)) : 0.0f};
+    }
+    __device__ __forceinline__ static void apply1(const FwdEpi &e, uint32_t m, uint32_t n, float v, const Col1 &col,
+                                                  uint32_t) {
+        float z = v;
+        if (e.bias) z = z + col.bias;   // f32 acc + f32(b), one rounding
+        const T zt = from_f32<T>(z);
+        const uint64_t idx = (uint64_t)m * e.ldc + n;
+        st_t<T>(e.z_out, idx, zt);
+        if (!e.fuse_act) return;
+        const float a = activation(e.act, to_f32(zt), e.leaky);
+        st_t<T>(e.predrop, idx, from_f32<T>(a));
+        if (e.use_dropout) {
+            if (dropout_u(n, m, e.seed + m * 7u) >= e.p) {
+                const float scale = 1.0f / (1.0f - e.p);
+                st_t<T>(e.mask, idx, from_f32<T>(scale));
+                st_t<T>(e.out, idx, from_f32<T>(a * scale));
+            } else {
+                st_t<T>(e.mask, idx, (T)0);
+                st_t<T>(e.out, idx, (T)0);
+            }
+        } else {
+            st_t<T>(e.out, idx, from_f32<T>(a));
+        }
+    }
     __device__ __forceinline__ static void apply(const FwdEpi &e, const GemmShape &sh, uint32_t m, uint32_t n,
                                                  floatx4 v, uint32_t) {
         if (m >= sh.M) return;
@@ -129,6 +157,12 @@ struct EpiStoreK {
                                                   const Col &, const Pre &) {
         __builtin_nontemporal_store(v, reinterpret_cast<floatx4 *>(e.out + idx));
     }
+    struct Col1 {};
+    __device__ __forceinline__ static Col1 column1(const StoreEpi &, uint32_t) { return Col1{}; }
+    __device__ __forceinline__ static void apply1(const StoreEpi &e, uint32_t m, uint32_t n, float v, const Col1 &,
+                                                  uint32_t split) {
+        e.out[(uint64_t)split * e.split_stride + (uint64_t)m * e.ldc + n] = v;
+    }
     __device__ __forceinline__ static void apply(const StoreEpi &e, const GemmShape &sh, uint32_t m, uint32_t n,
                                                  floatx4 v, uint32_t split) {
         if (m >= sh.M) return;
@@ -179,6 +213,19 @@ template <typename T> struct EpiOptK {
                 *reinterpret_cast<floatx4 *>(reinterpret_cast<T *>(e.param) + idx) = __builtin_bit_cast(floatx4, t);
             }
         }
+    }
+    struct Col1 {};
+    __device__ __forceinline__ static Col1 column1(const OptEpi &, uint32_t) { return Col1{}; }
+    __device__ __forceinline__ static void apply1(const OptEpi &e, uint32_t m, uint32_t n, float v, const Col1 &,
+                                                  uint32_t) {
+        const uint64_t idx = (uint64_t)m * e.ldc + n;
+        float pj = e.master[idx], vj = e.dv[idx], mj = e.dm[idx];
+        optimiser_step(pj, vj, mj, v * kLossScaleInv, e.inv_m, e.lr, e.clamp, e.opt, e.regularisation, e.regu_coeff,
+                       true);
+        e.master[idx] = pj;
+        e.dv[idx] = vj;
+        e.dm[idx] = mj;
+        if (e.param) st_t<T>(e.param, idx, from_f32<T>(pj));
     }
     __device__ __forceinline__ static void apply(const OptEpi &e, const GemmShape &sh, uint32_t m, uint32_t n,
                                                  floatx4 v, uint32_t) {

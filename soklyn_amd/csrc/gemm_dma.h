@@ -516,6 +516,15 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
     shv.N = sh.nv;
     const typename Epi::Params eps = Epi::at_split(ep, split);
     const typename Epi::Col col = EDGE ? typename Epi::Col{} : Epi::column(eps, n0 + c);
+    // EDGE: lane l's columns n0 + l + 64 q, their per-column operands loaded once
+    typename Epi::Col1 col1[4];
+    if constexpr (EDGE) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t n = n0 + lane + 64u * q;
+            col1[q] = n < shv.N ? Epi::column1(ep, n) : typename Epi::Col1{};
+        }
+    }
 #pragma unroll
     for (int pass = 0; pass < C::TWM / RPP; ++pass) {
 #pragma unroll
@@ -543,9 +552,10 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
         if constexpr (EDGE) {
             // element by element, lane l taking columns l, l + 64, l + 128, l + 192
             // of the row: each store instruction covers 64 consecutive columns
-            // whatever the output's alignment (Epi::apply with the column bound
-            // lowered to n + 1 handles exactly column n)
-#pragma unroll 1
+            // whatever the output's alignment; the per-column operands (bias)
+            // were loaded above, so a row is stores only (plus dW's per-element
+            // optimiser state)
+#pragma unroll 2
             for (int b = 0; b < ROWS_PER_THREAD; ++b) {
                 const uint32_t r = wave + (uint32_t)NW * b;
                 const uint32_t wmi = r / RPP, rr = r % RPP;
@@ -555,10 +565,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
                 for (int q = 0; q < 4; ++q) {
                     const uint32_t n = n0 + lane + 64u * q;
                     if (n >= shv.N) break;
-                    GemmShape one = shv;
-                    one.N = n + 1;
-                    const floatx4 v = {E[r * EPITCH + lane + 64u * q], 0.0f, 0.0f, 0.0f};
-                    Epi::apply(ep, one, m, n, v, split);
+                    Epi::apply1(ep, m, n, E[r * EPITCH + lane + 64u * q], col1[q], split);
                 }
             }
             if (pass + 1 < C::TWM / RPP) lds_barrier();

@@ -547,6 +547,113 @@ __global__ void __launch_bounds__(1024) skinny_fwd_kernel(GemmShape sh, const T 
     }
 }
 
+// The same on MFMA (fp16): a quad of 4 waves takes a block of 16 rows (one 16 x 16
+// output block, columns past N zero), wave w of the quad the k-chunks w, w + 4, ...
+// of 32 k, each a v_mfma_f32_16x16x32_f16 with lane l feeding X[row l % 16][k + 8
+// (l / 16) .. + 7] and W^T[column l % 16][same k] (LDS rows of P halves, P = 8
+// mod 128: the 16 rows of a read sit in distinct banks).  Rows that are not 16-byte
+// aligned are cut out of the two aligned 16-byte chunks covering them (funnel
+// shifts; the second chunk only when it holds a row element), k past K reads as
+// zero.  The quad's 4 partial blocks are added in wave order in LDS, and the
+// forward epilogue runs per element (lane l: rows 4 (l / 16) .. + 3 of column
+// l % 16, whose bias is loaded once).  One workgroup of 16 waves per CU stages W^T
+// once; every quad runs the same number of row-block rounds (barriers).
+constexpr uint32_t SKINNY_MFMA_P_MAX = 4104;   // LDS row pitch bound (K <= 4096): 16 rows + the sums fit 160 KB
+__device__ __forceinline__ halfx8 skinny_x8(const half_t *__restrict__ A, uint64_t rb, uint32_t k, uint32_t K,
+                                           uint64_t in_elems, bool vecx) {
+    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+    const uint64_t e = rb + k;
+    u32x4v v = {0, 0, 0, 0};
+    if (vecx) {
+        v = *reinterpret_cast<const u32x4v *>(A + e);
+    } else {
+        const uint64_t a0 = e & ~7ull;
+        const uint32_t sh = (uint32_t)(e - a0);   // halves past the aligned chunk
+        const u32x4v lo = *reinterpret_cast<const u32x4v *>(A + a0);
+        const u32x4v hi = (sh && a0 + 8 < in_elems) ? *reinterpret_cast<const u32x4v *>(A + a0 + 8) : u32x4v{0, 0, 0, 0};
+        const uint32_t w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        const uint32_t wd = sh >> 1, bits = (sh & 1u) * 16u;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            const uint32_t x0 = wd == 0 ? w[d] : wd == 1 ? w[d + 1] : wd == 2 ? w[d + 2] : w[d + 3];
+            const uint32_t x1 = wd == 0 ? w[d + 1] : wd == 1 ? w[d + 2] : wd == 2 ? w[d + 3] : w[d + 4];
+            v[d] = __builtin_amdgcn_alignbit(x1, x0, bits);   // (x1:x0) >> bits
+        }
+    }
+    halfx8 h = __builtin_bit_cast(halfx8, v);
+    if (k + 8 > K) {
+#pragma unroll
+        for (uint32_t i = 0; i < 8; ++i)
+            if (k + i >= K) h[i] = (_Float16)0.0f;
+    }
+    return h;
+}
+
+template <bool VECX>
+__global__ void __launch_bounds__(1024) skinny_fwd_mfma_kernel(GemmShape sh, const half_t *__restrict__ A,
+                                                               const half_t *__restrict__ B, FwdEpi ep, uint32_t P) {
+    __shared__ __attribute__((aligned(16))) half_t ws[SKINNY_N * SKINNY_MFMA_P_MAX];
+    __shared__ __attribute__((aligned(16))) float red[16][256];
+    const uint32_t K = sh.K, N = sh.N, M = sh.M;
+    const uint32_t Kc = (K + 31) / 32 * 32;
+    for (uint32_t i = threadIdx.x; i < SKINNY_N * Kc; i += blockDim.x) {
+        const uint32_t n = i / Kc, k = i - n * Kc;
+        ws[n * P + k] = (n < N && k < K) ? B[(uint64_t)k * sh.ldb + n] : (half_t)0;
+    }
+    __syncthreads();
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, quad = wave >> 2, wq = wave & 3u;
+    const uint32_t r16 = lane & 15u, kg = lane >> 4;
+    const uint32_t nblk = (M + 15) / 16, nck = Kc / 32;
+    const typename EpiFwdK<half_t>::Col1 c1 =
+        r16 < N ? EpiFwdK<half_t>::column1(ep, r16) : typename EpiFwdK<half_t>::Col1{};
+    const uint64_t in_elems = (uint64_t)(M - 1) * sh.lda + K;   // readable elements of X
+    const half_t *wrow = ws + r16 * P + kg * 8;
+    for (uint32_t base = blockIdx.x * 4; base < nblk; base += gridDim.x * 4) {
+        const uint32_t blk = base + quad;
+        floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (blk < nblk) {   // uniform in the wave: the MFMAs below run with every lane
+            const uint32_t m = blk * 16 + r16;
+            const bool mrow = m < M;   // rows past M feed zero fragments
+            const uint64_t rb = (uint64_t)(mrow ? m : 0u) * sh.lda;
+            // 4 of the wave's k-chunks per round: their loads first, then the MFMAs
+            for (uint32_t ck0 = wq; ck0 < nck; ck0 += 16) {
+                halfx8 xa[4], wb[4];
+#pragma unroll
+                for (uint32_t u = 0; u < 4; ++u) {
+                    const uint32_t ck = ck0 + 4 * u;   // same in every lane
+                    if (ck < nck) {
+                        const uint32_t k = ck * 32 + kg * 8;
+                        xa[u] = (mrow && k < K) ? skinny_x8(A, rb, k, K, in_elems, VECX && k + 8 <= K) : halfx8{};
+                        wb[u] = *reinterpret_cast<const halfx8 *>(wrow + ck * 32);
+                    } else {
+                        xa[u] = halfx8{};
+                        wb[u] = halfx8{};
+                    }
+                }
+#pragma unroll
+                for (uint32_t u = 0; u < 4; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[u], wb[u], acc, 0, 0, 0);
+            }
+        }
+        *reinterpret_cast<floatx4 *>(&red[wave][lane * 4]) = acc;
+        __syncthreads();
+        if (blk < nblk && wq == 0) {
+            const floatx4 p0 = *reinterpret_cast<const floatx4 *>(&red[quad * 4 + 0][lane * 4]);
+            const floatx4 p1 = *reinterpret_cast<const floatx4 *>(&red[quad * 4 + 1][lane * 4]);
+            const floatx4 p2 = *reinterpret_cast<const floatx4 *>(&red[quad * 4 + 2][lane * 4]);
+            const floatx4 p3 = *reinterpret_cast<const floatx4 *>(&red[quad * 4 + 3][lane * 4]);
+            const floatx4 sum = ((p0 + p1) + p2) + p3;
+#pragma unroll
+            for (uint32_t i = 0; i < 4; ++i) {
+                const uint32_t mo = blk * 16 + 4 * kg + i;
+                if (mo < M && r16 < N) EpiFwdK<half_t>::apply1(ep, mo, r16, sum[i], c1, 0);
+            }
+        }
+        __syncthreads();   // red is rewritten by the next round
+    }
+}
+
+static uint32_t skinny_mfma_pitch(uint32_t K) { return (K + 127) / 128 * 128 + 8; }
+
 bool skinny_fwd_ok(const GemmLaunch &g) {
     const size_t esz = g.dtype == 1 ? 2 : 4;
     const size_t kp = (g.K + 7) / 8 * 8;
@@ -556,6 +663,20 @@ bool skinny_fwd_ok(const GemmLaunch &g) {
 
 template <typename T> static void launch_skinny_fwd_t(const GemmShape &sh, const GemmLaunch &g, hipStream_t s) {
     const bool vecx = sh.lda % 8 == 0 && (reinterpret_cast<uintptr_t>(g.A) & 15u) == 0;
+    if constexpr (sizeof(T) == 2) {
+        const uint32_t P = skinny_mfma_pitch(sh.K);
+        // the MFMA kernel reads 16-byte chunks of X: a 16-byte aligned base
+        if (P <= SKINNY_MFMA_P_MAX && (reinterpret_cast<uintptr_t>(g.A) & 15u) == 0 && sh.M > 0) {
+            uint32_t grid = (sh.M + 63) / 64;   // 4 blocks of 16 rows per workgroup and round
+            if (grid > 256) grid = 256;
+            const half_t *A = reinterpret_cast<const half_t *>(g.A), *B = reinterpret_cast<const half_t *>(g.B);
+            if (vecx)
+                launch_timed(g, skinny_fwd_mfma_kernel<true>, dim3(grid), dim3(1024), s, sh, A, B, g.fwd, P);
+            else
+                launch_timed(g, skinny_fwd_mfma_kernel<false>, dim3(grid), dim3(1024), s, sh, A, B, g.fwd, P);
+            return;
+        }
+    }
     uint32_t grid = (sh.M + 15) / 16;   // 16 waves per workgroup, a row per wave at a time
     if (grid > 256) grid = 256;
     const T *A = reinterpret_cast<const T *>(g.A), *B = reinterpret_cast<const T *>(g.B);

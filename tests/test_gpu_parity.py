@@ -68,6 +68,11 @@ FWD_CASES = [
     (130, 40, 3001, 1, 7, 0.0),     # RMSNorm + Mish
     (70, 32, 1022, 2, 6, 0.0),      # LN + SiLU, width 2 mod 4
     (50, 24, 4093, 1, 4, 0.2),      # RMSNorm + Tanh + dropout, 4 groups per thread
+    # outputs of <= 16 columns (the skinny forward): odd K (rows not 16-byte
+    # aligned, a partial last k-chunk), a partial last block of 16 rows, dropout;
+    # and K a multiple of 8 (16-byte row loads) over several rounds of row blocks
+    (1000, 3001, 13, 0, 1, 0.1),    # Sigmoid + dropout
+    (4100, 2048, 10, 0, 2, 0.0),    # ReLU
 ]
 
 

@@ -596,9 +596,20 @@ __global__ void __launch_bounds__(1024) skinny_fwd_mfma_kernel(GemmShape sh, con
     __shared__ __attribute__((aligned(16))) float red[16][256];
     const uint32_t K = sh.K, N = sh.N, M = sh.M;
     const uint32_t Kc = (K + 31) / 32 * 32;
-    for (uint32_t i = threadIdx.x; i < SKINNY_N * Kc; i += blockDim.x) {
-        const uint32_t n = i / Kc, k = i - n * Kc;
-        ws[n * P + k] = (n < N && k < K) ? B[(uint64_t)k * sh.ldb + n] : (half_t)0;
+    // W^T staging: 8 element loads in flight per thread (W is read as stored,
+    // row k of N halves)
+    for (uint32_t i0 = threadIdx.x; i0 < SKINNY_N * Kc; i0 += 8 * blockDim.x) {
+        half_t v[8];
+#pragma unroll
+        for (uint32_t u = 0; u < 8; ++u) {
+            const uint32_t i = i0 + u * blockDim.x, k = i / SKINNY_N, n = i % SKINNY_N;
+            v[u] = (i < SKINNY_N * Kc && n < N && k < K) ? B[(uint64_t)k * sh.ldb + n] : (half_t)0;
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < 8; ++u) {
+            const uint32_t i = i0 + u * blockDim.x, k = i / SKINNY_N, n = i % SKINNY_N;
+            if (i < SKINNY_N * Kc) ws[n * P + k] = v[u];
+        }
     }
     __syncthreads();
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, quad = wave >> 2, wq = wave & 3u;
@@ -703,12 +714,13 @@ hipError_t launch_skinny_fwd(const GemmLaunch &g, hipStream_t s) {
 
 // dW partial sums, thread per W row: thread k of workgroup (x, y) walks the batch rows
 // of slice y in order, acc[n] += X[b][k] * dP[b][n], with 64 rows of dP (fp32) at a
-// time in LDS (broadcast reads); partials[y][k][0..15].
+// time in LDS (16-byte broadcast reads) and the X loads of 16 rows issued before
+// their FMAs; partials[y][k][0..15].
 template <typename T> __global__ void __launch_bounds__(256) skinny_dw_kernel(GemmShape sh, const T *__restrict__ X,
                                                                              const float *__restrict__ dp,
                                                                              float *__restrict__ partials,
                                                                              uint32_t per) {
-    __shared__ float dps[64][SKINNY_N];
+    __shared__ __attribute__((aligned(16))) float dps[64][SKINNY_N];
     const uint32_t K = sh.M, N = sh.N;          // output [K x N]; reduction over sh.K batch rows
     const uint32_t k = blockIdx.x * 256 + threadIdx.x;
     const uint32_t r0 = blockIdx.y * per;
@@ -725,11 +737,23 @@ template <typename T> __global__ void __launch_bounds__(256) skinny_dw_kernel(Ge
         }
         __syncthreads();
         if (k < K) {
-#pragma unroll 4
-            for (uint32_t r = 0; r < nrows; ++r) {
-                const float xv = to_f32(X[(uint64_t)(rb + r) * sh.lda + k]);
+            for (uint32_t r0b = 0; r0b < nrows; r0b += 16) {
+                float xv[16];
 #pragma unroll
-                for (int n = 0; n < (int)SKINNY_N; ++n) acc[n] = fmaf(xv, dps[r][n], acc[n]);
+                for (uint32_t u = 0; u < 16; ++u)
+                    xv[u] = r0b + u < nrows ? to_f32(X[(uint64_t)(rb + r0b + u) * sh.lda + k]) : 0.0f;
+#pragma unroll
+                for (uint32_t u = 0; u < 16; ++u) {
+                    if (r0b + u >= nrows) break;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const floatx4 d = *reinterpret_cast<const floatx4 *>(&dps[r0b + u][4 * q]);
+                        acc[4 * q + 0] = fmaf(xv[u], d[0], acc[4 * q + 0]);
+                        acc[4 * q + 1] = fmaf(xv[u], d[1], acc[4 * q + 1]);
+                        acc[4 * q + 2] = fmaf(xv[u], d[2], acc[4 * q + 2]);
+                        acc[4 * q + 3] = fmaf(xv[u], d[3], acc[4 * q + 3]);
+                    }
+                }
             }
         }
     }

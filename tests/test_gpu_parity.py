@@ -73,6 +73,9 @@ FWD_CASES = [
     # and K a multiple of 8 (16-byte row loads) over several rounds of row blocks
     (1000, 3001, 13, 0, 1, 0.1),    # Sigmoid + dropout
     (4100, 2048, 10, 0, 2, 0.0),    # ReLU
+    # ragged 256x256 path at C5's first-layer shape (294 tiles, padded operands,
+    # element-wise epilogue) with the fused activation and dropout
+    (12345, 777, 1531, 0, 6, 0.1),  # SiLU + dropout
 ]
 
 

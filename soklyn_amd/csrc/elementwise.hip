@@ -930,7 +930,7 @@ __global__ void __launch_bounds__(256) colsum_kernel(VecOptArgs a) {
 // a.cpb columns per workgroup (a power of 2), 256 / cpb lanes per column: lane j
 // sums the partials of splits j, j + lanes, ... in order (8 loads in flight), then
 // the lanes of a column are added in a fixed tree (halving strides).  cpb comes
-// from vec_opt_cpb: about 8 splits per lane.
+// from vec_opt_cpb: at most 16 splits per lane.
 template <typename T> __device__ __forceinline__ void vec_opt_block(const VecOptArgs &a, uint32_t block) {
     __shared__ float red[3][256];
     const uint32_t cpb = a.cpb, lanes = 256u / cpb;
@@ -1025,10 +1025,10 @@ uint32_t colsum_splits(uint32_t rows, uint32_t n) {
 }
 
 // Columns per workgroup of the parameter update: lanes per column doubled from 16
-// (up to 256) until a lane has at most 8 of the `splits` partial rows to add.
+// (up to 256) until a lane has at most 16 of the `splits` partial rows to add.
 uint32_t vec_opt_cpb(uint32_t splits) {
     uint32_t lanes = 16;
-    while (lanes < 256 && lanes * 8 < splits) lanes *= 2;
+    while (lanes < 256 && lanes * 16 < splits) lanes *= 2;
     return 256 / lanes;
 }
 

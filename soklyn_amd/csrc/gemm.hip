@@ -764,6 +764,66 @@ template <typename T> __global__ void __launch_bounds__(256) skinny_dw_kernel(Ge
         *reinterpret_cast<floatx4 *>(p + 4 * q) = floatx4{acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]};
 }
 
+// The same on MFMA (fp16; dP as its fp16 copy, the dW GEMMs' operand): thread t
+// of workgroup (x, y) loads column k = 256 x + t of X for 32 batch rows at a time
+// (coalesced 2-byte loads, all 32 issued before use) and writes them to LDS
+// transposed (xt[t][0..31], one 64-byte run); the 32 x 16 block of dP goes to
+// pt[n][0..31].  Wave w then runs v_mfma_f32_16x16x32_f16 on its 4 tiles of 16 W
+// rows: src0 lane l = xt[16 q + l % 16][8 (l / 16) ..] (X^T), src1 lane l =
+// pt[l % 16][8 (l / 16) ..] (dP); lane l ends with rows 4 (l / 16) .. + 3 of column
+// l % 16 of the tile.  LDS rows of 40 halves (80 bytes) keep the 16-byte reads of
+// 16 lanes in distinct banks.  partials[y][k][0..15] as in skinny_dw_kernel.
+__global__ void __launch_bounds__(256) skinny_dw_mfma_kernel(GemmShape sh, const half_t *__restrict__ X,
+                                                             const half_t *__restrict__ dp16,
+                                                             float *__restrict__ partials, uint32_t per) {
+    __shared__ __attribute__((aligned(16))) half_t xt[256][40];
+    __shared__ __attribute__((aligned(16))) half_t pt[SKINNY_N][40];
+    const uint32_t K = sh.M, N = sh.N;          // output [K x N]; reduction over sh.K batch rows
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t k0 = blockIdx.x * 256, k = k0 + tid;
+    const uint32_t r0 = blockIdx.y * per;
+    const uint32_t r1 = min(sh.K, r0 + per);
+    floatx4 acc[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) acc[q] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t rb = r0; rb < r1; rb += 32) {
+        const uint32_t nrows = min(32u, r1 - rb);
+        half_t xv[32];
+#pragma unroll
+        for (uint32_t u = 0; u < 32; ++u)
+            xv[u] = (u < nrows && k < K) ? X[(uint64_t)(rb + u) * sh.lda + k] : (half_t)0;
+        half_t pv[2];
+#pragma unroll
+        for (uint32_t h = 0; h < 2; ++h) {
+            const uint32_t i = tid + 256 * h, u = i >> 4, n = i & 15u;   // 32 rows x 16 columns
+            pv[h] = (u < nrows && n < N) ? dp16[(uint64_t)(rb + u) * sh.ldb + n] : (half_t)0;
+        }
+        __syncthreads();   // the previous block's fragments are read
+#pragma unroll
+        for (int q = 0; q < 4; ++q) *reinterpret_cast<halfx8 *>(&xt[tid][8 * q]) = *reinterpret_cast<const halfx8 *>(&xv[8 * q]);
+#pragma unroll
+        for (uint32_t h = 0; h < 2; ++h) {
+            const uint32_t i = tid + 256 * h;
+            pt[i & 15u][i >> 4] = pv[h];
+        }
+        __syncthreads();
+        const halfx8 b = *reinterpret_cast<const halfx8 *>(&pt[lane & 15u][8 * (lane >> 4)]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const halfx8 a = *reinterpret_cast<const halfx8 *>(&xt[wave * 64 + 16 * q + (lane & 15u)][8 * (lane >> 4)]);
+            acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[q], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+        for (uint32_t r = 0; r < 4; ++r) {
+            const uint32_t ko = k0 + wave * 64 + 16 * q + 4 * (lane >> 4) + r;
+            if (ko < K) partials[((uint64_t)blockIdx.y * K + ko) * SKINNY_N + (lane & 15u)] = acc[q][r];
+        }
+    }
+}
+
 uint32_t skinny_dw_slices(uint32_t rows, uint32_t K) {
     const uint32_t col_blocks = (K + 255) / 256;
     uint32_t sl = (1024 + col_blocks - 1) / col_blocks;
@@ -783,7 +843,11 @@ hipError_t launch_skinny_dw(const GemmLaunch &g, float *partials, uint32_t slice
     sh.ldb = g.N;        // d_prenorm row pitch
     const uint32_t per = (g.K + slices - 1) / slices;
     const dim3 grid((g.M + 255) / 256, slices);
-    if (g.dtype == 1)
+    if (g.dtype == 1 && g.B) {
+        // fp16: MFMA on the fp16 copy of d_prenorm (row pitch N)
+        launch_timed(g, skinny_dw_mfma_kernel, grid, dim3(256), s, sh, reinterpret_cast<const half_t *>(g.A),
+                     reinterpret_cast<const half_t *>(g.B), partials, per);
+    } else if (g.dtype == 1)
         launch_timed(g, skinny_dw_kernel<half_t>, grid, dim3(256), s, sh, reinterpret_cast<const half_t *>(g.A),
                      g.b32, partials, per);
     else

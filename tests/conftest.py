@@ -25,3 +25,16 @@ def ctx():
     yield c
     torch.cuda.synchronize()
     c.close()
+
+
+def pytest_sessionfinish(session, exitstatus):
+    """Write every parity check's metrics to $SOKLYN_PARITY_REPORT (JSON lines), when set."""
+    path = os.environ.get("SOKLYN_PARITY_REPORT")
+    if not path:
+        return
+    import json
+    from tests import helpers
+    os.makedirs(os.path.dirname(os.path.abspath(path)), exist_ok=True)
+    with open(path, "w") as f:
+        for r in helpers.RECORDS:
+            f.write(json.dumps(r) + "\n")

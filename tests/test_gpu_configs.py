@@ -11,7 +11,7 @@ the GPU box's host cores).
 
 Single blocks take one step of forward -> act' of a supplied upstream gradient ->
 dW + optimiser -> dX (bench.py's step); the MLPs take FeedForwardNetwork's step.
-Gates as everywhere: fp32 1e-4, fp16 2e-2 normwise; dropout masks bit-exact.
+Gates as everywhere: fp32 1e-4 elementwise, fp16 2e-2 normwise; dropout masks bit-exact.
 
 Each stage is checked on identical inputs: after the forward has been compared, the
 device's forward caches are copied into the oracle blocks before the backward.  At
@@ -28,7 +28,7 @@ import torch
 from oracle import oracle as O
 from soklyn_amd import abi
 from soklyn_amd.devblock import DeviceBlock
-from tests.helpers import FP16_TOL, FP32_TOL, f16, he_normal, normwise, rng
+from tests.helpers import FP16_TOL, FP32_TOL, check, f16, he_normal, rng
 from tests.test_gpu_ffn import build_net
 
 pytestmark = pytest.mark.gpu
@@ -40,12 +40,6 @@ def sync_caches(ob, db):
     """Give the oracle block the device's forward caches (the backward's inputs)."""
     for n in CACHES:
         setattr(ob, n, np.ascontiguousarray(db.get(n), np.float32).reshape(getattr(ob, n).shape))
-
-
-def check(name, a, r, tol):
-    e = normwise(a, r)
-    print(f"  {name}: {e:.2e}", flush=True)
-    assert e <= tol, f"{name}: normwise error {e:.3e} > {tol:.1e}"
 
 
 def single_block_step(ctx, M, K, N, half, act, opt_o, opt_d, lr):

@@ -14,7 +14,7 @@ import torch
 from oracle import oracle as O
 from soklyn_amd import abi
 from soklyn_amd.devblock import DeviceBlock
-from tests.helpers import FP16_TOL, FP32_TOL, f16, he_normal, normwise, rng
+from tests.helpers import FP16_TOL, FP32_TOL, check, f16, he_normal, rng
 
 pytestmark = pytest.mark.gpu
 
@@ -62,11 +62,9 @@ def device_step(dbs, x, t, M, loss, loss_act, opt, lr, step, use_dropout, seeds)
 def compare_nets(obs, dbs, M, tol, half):
     for i, (ob, db) in enumerate(zip(obs, dbs)):
         for n in ("out", "preact", "grad", "d_prenorm", "dv_w", "dm_w", "dv_b"):
-            e = normwise(db.get(n), getattr(ob, n))
-            assert e <= tol, f"layer {i} {n}: {e:.3e}"
+            check(f"layer {i} {n}", db.get(n), getattr(ob, n), tol)
         wn = "master_w" if half else "w"
-        e = normwise(db.get(wn), getattr(ob, wn))
-        assert e <= tol, f"layer {i} {wn}: {e:.3e}"
+        check(f"layer {i} {wn}", db.get(wn), getattr(ob, wn), tol)
 
 
 def test_c1_mlp_fp32_sgd(ctx):
@@ -124,8 +122,7 @@ def test_c4_like_rms_mish_dropout_fp16_small(ctx):
         assert np.array_equal(db.get("mask"), ob.mask)
     for i, (ob, db) in enumerate(zip(obs, dbs)):
         for n in ("out", "d_prenorm", "dm_w", "dv_w"):
-            e = normwise(db.get(n), getattr(ob, n))
-            assert e <= FP16_TOL, f"layer {i} {n}: {e:.3e}"
+            check(f"layer {i} {n}", db.get(n), getattr(ob, n), FP16_TOL)
 
 
 def test_c5_like_ragged_ln_leaky_bce_fp16_small(ctx):
@@ -143,5 +140,4 @@ def test_c5_like_ragged_ln_leaky_bce_fp16_small(ctx):
     torch.cuda.synchronize()
     for i, (ob, db) in enumerate(zip(obs, dbs)):
         for n in ("out", "d_prenorm", "dm_w", "dv_w", "dm_norm_w"):
-            e = normwise(db.get(n), getattr(ob, n))
-            assert e <= FP16_TOL, f"layer {i} {n}: {e:.3e}"
+            check(f"layer {i} {n}", db.get(n), getattr(ob, n), FP16_TOL)

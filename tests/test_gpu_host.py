@@ -18,7 +18,7 @@ import pytest
 
 from oracle import oracle as O
 from soklyn_amd import abi
-from tests.helpers import FP16_TOL, FP32_TOL, f16, normwise, rng
+from tests.helpers import FP16_TOL, FP32_TOL, check, f16, rng
 from tests.test_gpu_ffn import oracle_step
 from tests.test_safetensors_cpu import serde_pretty_header
 
@@ -111,8 +111,7 @@ def compare(obs, res, tol, half, masks):
     for i, ob in enumerate(obs):
         for n in ("out", "grad", "d_prenorm", "dv_w", "dm_w", "dv_b", "master_w" if half else "w"):
             ref = np.asarray(getattr(ob, n), np.float32).reshape(-1)
-            e = normwise(res[(n, i)], ref)
-            assert e <= tol, f"layer {i} {n}: {e:.3e}"
+            check(f"layer {i} {n}", res[(n, i)], ref, tol)
         if masks and i < len(obs) - 1:
             assert np.array_equal(res[("mask", i)], np.asarray(ob.mask, np.float32).reshape(-1)), f"layer {i} mask"
 

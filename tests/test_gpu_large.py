@@ -9,7 +9,7 @@ import torch
 from oracle import oracle as O
 from soklyn_amd import abi
 from soklyn_amd.devblock import DeviceBlock
-from tests.helpers import FP16_TOL, FP32_TOL, f16, he_normal, normwise, rng
+from tests.helpers import FP16_TOL, FP32_TOL, check, f16, he_normal, rng
 
 pytestmark = pytest.mark.gpu
 
@@ -38,8 +38,7 @@ def test_forward_large_tiles(ctx, half, M, K, N):
     torch.cuda.synchronize()
     tol = FP16_TOL if half else FP32_TOL
     for n in ("preact", "out"):
-        e = normwise(db.get(n), getattr(ob, n))
-        assert e <= tol, f"{n}: {e:.3e}"
+        check(f"{n}", db.get(n), getattr(ob, n), tol)
 
 
 @pytest.mark.parametrize("half,M,K,N", [(True, BIG, BIG, 256), (False, 2048, 2048, 256)])
@@ -54,8 +53,7 @@ def test_input_grad_large_tiles(ctx, half, M, K, N):
     db.error_from_sum(torch.from_numpy(s).cuda(), M)
     dx = db.input_grad(M)
     torch.cuda.synchronize()
-    e = normwise(dx.cpu().numpy(), ob.input_grad(M))
-    assert e <= (FP16_TOL if half else FP32_TOL), f"input_grad: {e:.3e}"
+    check(f"input_grad", dx.cpu().numpy(), ob.input_grad(M), (FP16_TOL if half else FP32_TOL))
 
 
 @pytest.mark.parametrize("half,M,K,N", [(True, 256, BIG, BIG), (False, 256, 2048, 2048)])
@@ -73,8 +71,7 @@ def test_backward_large_tiles(ctx, half, M, K, N):
     torch.cuda.synchronize()
     tol = FP16_TOL if half else FP32_TOL
     for n in ("dv_w", "dv_b"):
-        e = normwise(db.get(n), getattr(ob, n))
-        assert e <= tol, f"{n}: {e:.3e}"
+        check(f"{n}", db.get(n), getattr(ob, n), tol)
 
 
 # The 256x256 tiles also carry the fused epilogues with dropout, with the

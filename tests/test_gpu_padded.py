@@ -8,7 +8,7 @@ kernel, each at a moderate size the oracle finishes in a second or two:
     optimiser kernel reduces the fp32 partial planes;
   * the hidden error is the dX GEMM into the workspace, then the error kernel.
 
-Gates as everywhere: fp16 2e-2 normwise against the oracle; dropout masks bit-exact.
+Gates as everywhere: fp16 2e-2 normwise (elementwise reported) against the oracle; dropout masks bit-exact.
 """
 from __future__ import annotations
 

@@ -293,6 +293,90 @@ def test_batch_norm_gradient_hand_values():
     assert np.allclose(ob.d_prenorm, -256.0)
 
 
+def _norm_grad_block(norm, e, M=2, N=4, p=2.0, c=2.0, rstd=0.5, nw=1.5):
+    """M x N output block whose error is e everywhere (MSE + identity: e = out - target, target 0),
+    prenorm p and centered c set apart so that a formula reading the wrong one fails."""
+    ob = O.OracleBlock(1, N, M, np.zeros((1, N), np.float32), norm=norm, act=0)
+    ob.prenorm[:] = p
+    ob.centered[:] = c
+    ob.norm_rstd[:] = rstd
+    ob.norm_w[:] = nw
+    ob.out[:] = e
+    ob.preact[:] = 1.0
+    ob.output_error(np.zeros((M, N), np.float32), 0, 0)
+    return ob
+
+
+# Hand values with e != 1 (util.cu:187-210, Q3).  With e = 1 the reference's
+# missing e factor in the RMS second term, and the e factor of the LN / BN third
+# term, cannot be seen; each case below names the value the "fixed" formula
+# would give, which the oracle must NOT produce.  Common: g = 1.5, rstd = 0.5,
+# N = 4; the output layer's d_prenorm carries LOSS_SCALE = 512, dNorm does not.
+@pytest.mark.parametrize("e,d,d_fixed,dnw", [
+    # RMS, p = 2 (c = 7 ignored): d = g r (e - r^2 p^2 / N) = 0.75 (e - 0.25)
+    (2.0, 0.75 * 1.75, 0.75 * (2.0 - 0.5), 2.0),          # 672;  e r^2 p^2 / N would give 576
+    (-0.5, 0.75 * -0.75, 0.75 * (-0.5 + 0.125), -0.5),    # -288; e r^2 p^2 / N would give -144
+])
+def test_rms_norm_gradient_hand_values_e_not_one(e, d, d_fixed, dnw):
+    ob = _norm_grad_block(1, e, p=2.0, c=7.0)
+    assert np.all(ob.d_prenorm == np.float32(512 * d))
+    assert not np.any(ob.d_prenorm == np.float32(512 * d_fixed))
+    assert np.all(ob.d_norm_w == np.float32(dnw))          # dNw = e p rstd
+    assert not ob.d_norm_b.any()
+
+
+@pytest.mark.parametrize("e,d,d_fixed,dnw", [
+    # LN, c = 2 (p = 5 ignored): d = g r (e - e / N - r^2 c^2 e / N) = 0.75 (e - e/4 - e/4)
+    (2.0, 0.75 * (2.0 - 0.5 - 0.5), 0.75 * (2.0 - 0.5 - 0.25), 2.0),          # 384; without e: 480
+    (-0.5, 0.75 * (-0.5 + 0.125 + 0.125), 0.75 * (-0.5 + 0.125 - 0.25), -0.5),  # -96; without e: -240
+])
+def test_layer_norm_gradient_hand_values_e_not_one(e, d, d_fixed, dnw):
+    ob = _norm_grad_block(2, e, p=5.0, c=2.0)
+    assert np.all(ob.d_prenorm == np.float32(512 * d))
+    assert not np.any(ob.d_prenorm == np.float32(512 * d_fixed))
+    assert np.all(ob.d_norm_w == np.float32(dnw))          # dNw = e c rstd
+    assert np.all(ob.d_norm_b == np.float32(e))            # dNb = e
+
+
+@pytest.mark.parametrize("e,d,d_fixed,d_inv_n", [
+    # BN over m = 2 rows, c = 1 (p = 5 ignored): d = g r (e - e / m - r^2 c^2 e / m) = 0.75 (e - e/2 - e/8)
+    (2.0, 0.75 * (2.0 - 1.0 - 0.25), 0.75 * (2.0 - 1.0 - 0.125), 0.75 * (2.0 - 0.5 - 0.125)),
+    (-0.5, 0.75 * (-0.5 + 0.25 + 0.0625), 0.75 * (-0.5 + 0.25 - 0.125), 0.75 * (-0.5 + 0.125 + 0.03125)),
+])
+def test_batch_norm_gradient_hand_values_e_not_one(e, d, d_fixed, d_inv_n):
+    ob = _norm_grad_block(3, e, M=2, N=4, p=5.0, c=1.0)
+    assert np.all(ob.d_prenorm == np.float32(512 * d))
+    assert not np.any(ob.d_prenorm == np.float32(512 * d_fixed))     # third term without e
+    assert not np.any(ob.d_prenorm == np.float32(512 * d_inv_n))     # 1/N (columns) instead of 1/m (rows)
+    assert np.all(ob.d_norm_w == np.float32(e * 1.0 * 0.5))
+    assert np.all(ob.d_norm_b == np.float32(e))
+
+
+def test_rms_forward_fp16_rounds_twice():
+    """forward.cu:61-72 with T = half: preact = T(T(prenorm * rstd) * norm_w), rstd = T(rsqrt(...)).
+    One row of four f16 values (x = [1], W = that row), worked by hand in exact fractions:
+    sum z^2 / 4 + 1e-6 -> rstd32 = 0.197476 -> T: 809/4096.  Element 0:
+    z r = 837/128 * 809/4096 = 1322.52 / 1024 -> 1323/1024; * 351/512 = 1813.96 / 2048 -> 907/1024.
+    One rounding of z r g = 1813.30 / 2048 would give 1813/2048 instead."""
+    z = np.array([[837 / 128, 675 / 256, 927 / 256, 807 / 128]], np.float32)
+    gw = np.array([[351 / 512, 977 / 1024, 703 / 1024, 151 / 128]], np.float32)
+    ob = O.OracleBlock(1, 4, 1, z, half=True, norm=1, act=0)
+    ob.norm_w[:] = gw
+    ob.forward(np.ones((1, 1), np.float32), 1)
+    assert ob.norm_rstd[0] == np.float32(809 / 4096)
+    assert np.array_equal(ob.prenorm, z) and np.array_equal(ob.centered, z)
+    twice = np.array([[907 / 1024, 509 / 1024, 503 / 1024, 47 / 32]], np.float32)
+    once = np.array([[1813 / 2048, 2035 / 4096, 2011 / 4096, 47 / 32]], np.float32)
+    assert np.array_equal(ob.preact, twice)
+    assert np.sum(ob.preact != once) == 3
+    # the fp32 block rounds nowhere: z * rstd32 * g in f32 (rstd not rounded to f16)
+    o32 = O.OracleBlock(1, 4, 1, z, norm=1, act=0)
+    o32.norm_w[:] = gw
+    o32.forward(np.ones((1, 1), np.float32), 1)
+    assert abs(o32.norm_rstd[0] - 0.197476) < 1e-6
+    assert np.allclose(o32.preact, z * o32.norm_rstd[0] * gw, rtol=1e-6, atol=0)
+
+
 # ---- hidden error / input gradient ---------------------------------------------------------------------
 def test_hidden_error_and_input_grad_closed_form():
     M, K0, N0, N1 = 30, 12, 20, 7

@@ -138,6 +138,20 @@ def dropout_seeds(cfg, step):
             for i in range(len(cfg["dims"]) - 1)]
 
 
+def host_cpu():
+    """The CPU the baseline runs on: its model (/proc/cpuinfo) and the cores this process may use."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "host_cores_available": len(os.sched_getaffinity(0))}
+
+
 def cpu_baseline_block(cfg, rows: int, reps: int = 3):
     """The oracle (C restatement, fp32, OpenMP over the host cores) on the same step:
     one warm-up pass, then the median of `reps` timed passes."""
@@ -163,8 +177,10 @@ def cpu_baseline_block(cfg, rows: int, reps: int = 3):
     dt = times[len(times) // 2]
     flops = 3 * 2.0 * rows * K * N
     return {"value": round(flops / dt / 1e12, 6), "unit": "TFLOP/s", "cores": O.num_threads(), "kind": "port",
+            **host_cpu(),
             "sample": f"{rows} of {cfg['M']} batch rows of the same step (fwd, act', dW+update, dX) in fp32 "
-                      f"on the oracle; median of {reps} passes after one warm-up, {dt:.2f} s per pass"}
+                      f"on the oracle (OpenMP, {O.num_threads()} threads); median of {reps} passes after one "
+                      f"warm-up, {dt:.2f} s per pass"}
 
 
 def cpu_baseline_mlp(cfg, rows: int, reps: int = 3):
@@ -197,9 +213,10 @@ def cpu_baseline_mlp(cfg, rows: int, reps: int = 3):
     times = sorted(one(2 + i) for i in range(reps))
     dt = times[len(times) // 2]
     return {"value": round(mlp_flops(dims, rows) / dt / 1e12, 6), "unit": "TFLOP/s", "cores": O.num_threads(),
-            "kind": "port",
+            "kind": "port", **host_cpu(),
             "sample": f"{rows} of {cfg['M']} batch rows of the same train step (all layers fwd, loss, bwd + Adam) "
-                      f"in fp32 on the oracle; median of {reps} passes after one warm-up, {dt:.2f} s per pass"}
+                      f"in fp32 on the oracle (OpenMP, {O.num_threads()} threads); median of {reps} passes after "
+                      f"one warm-up, {dt:.2f} s per pass"}
 
 
 def timing_events(n):
@@ -215,7 +232,9 @@ def timing_events(n):
 class BlockBench:
     """Single DenseBlock: forward -> error_from_sum -> backward -> input_grad."""
     calls = ("forward", "error_from_sum", "backward", "input_grad")
-    gemms = ("forward_gemm", "dx_gemm")   # GEMM kernels timed alone (the roofline candidates)
+    # GEMM kernels timed alone (the roofline candidates): forward (+bias, act), dW (+ the
+    # optimiser step on W in its epilogue) and dX
+    gemms = ("forward_gemm", "dw_gemm", "dx_gemm")
 
     def __init__(self, cfg, ctx, stream):
         import torch
@@ -235,8 +254,16 @@ class BlockBench:
         self.M = M
         self.step_no = 0
         self.flops = 3 * 2.0 * M * K * N
-        self.kernel_flops = {"forward_gemm": 2.0 * M * K * N, "dx_gemm": 2.0 * M * K * N}
+        self.kernel_flops = {g: 2.0 * M * K * N for g in self.gemms}
         self.stream, self.ctx = stream, ctx
+        # error_from_sum is one element-wise kernel: its algorithmic HBM bytes (the
+        # activation derivative reads predrop for sigmoid / ReLU / leaky ReLU / tanh /
+        # SiLU and preact for SiLU / Mish; the mask always)
+        act, ts = cfg["act"], 2 if half else 4
+        reads = 4 + ts * (int(act in (ACT_SIGMOID, ACT_RELU, ACT_LEAKY, 4, ACT_SILU))
+                          + int(act in (ACT_SILU, ACT_MISH)) + 1)
+        writes = 4 + 4 + (2 if half else 0)       # grad, d_prenorm (fp32), d_prenorm_h (fp16 blocks)
+        self.hbm_bytes = {"error_from_sum": float(M) * N * (reads + writes)}
 
     def step(self, ev=None, gev=None):
         # ev: per-call (start, end) HIP events on the launch stream (a diagnostic pass
@@ -246,7 +273,7 @@ class BlockBench:
         b, M = self.blk, self.M
         fns = (lambda: b.forward(self.x, M), lambda: b.error_from_sum(self.dy, M),
                lambda: b.backward(self.x, self.tc, self.step_no), lambda: b.input_grad(M, self.dx))
-        gemm_of = {0: 0, 3: 1}
+        gemm_of = {0: 0, 2: 1, 3: 2}
         for i, fn in enumerate(fns):
             if gev is not None and i in gemm_of:
                 self.ctx.time_next_gemm(*gev[gemm_of[i]])
@@ -286,6 +313,7 @@ class MlpBench:
         self.calls = (f"hidden_error_layer{k}",)
         self.gemms = (self.timed,)
         self.kernel_flops = {self.timed: 2.0 * M * dims[k + 1] * dims[k + 2]}
+        self.hbm_bytes = {}
         self.ctx = ctx
 
     def step(self, ev=None, gev=None):
@@ -395,6 +423,12 @@ def main():
                      "kernel_ms": {k: round(v, 4) for k, v in kern.items()},
                      "call_ms": {k: round(v, 4) for k, v in call_ms.items()}},
     }
+    # bandwidth-bound calls made of one element-wise kernel: algorithmic bytes / call time
+    if bench.hbm_bytes:
+        out["hbm_kernels"] = {
+            c: {"bytes": int(b), "ms": round(call_ms[c], 4), "GB/s": round(b / (call_ms[c] * 1e-3) / 1e9, 1),
+                "frac_of_8TB/s": round(b / (call_ms[c] * 1e-3) / 8e12, 4)}
+            for c, b in bench.hbm_bytes.items()}
     if not args.no_cpu:
         if cfg["kind"] == "block":
             out["cpu_baseline"] = cpu_baseline_block(cfg, args.cpu_rows or cfg["M"])

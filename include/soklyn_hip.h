@@ -146,7 +146,8 @@ int32_t skl_memcpy_d2d(skl_ctx *ctx, void *dst, const void *src, size_t bytes);
 /* ---- utility kernels (util_device.rs) --------------------------------------- */
 /* gpu_broadcast (util_device.rs:49-78): dst[0..n) = v in dtype */
 int32_t skl_fill(skl_ctx *ctx, void *dst, uint32_t dtype, float v, size_t n);
-/* gpu_cast_t (util_device.rs:7-47): f32<->f16 (RNE); same-type is a copy */
+/* gpu_cast_t (util_device.rs:7-47): f32 -> f16 (round to nearest even) or f16 -> f32;
+ * any other pairing, same-type included, is SKL_ERR_UNSUPPORTED_CAST (util_device.rs:23-32) */
 int32_t skl_cast(skl_ctx *ctx, const void *src, uint32_t src_dtype, void *dst, uint32_t dst_dtype,
                  size_t n);
 /* scramble_seed (util/core.rs:90-94), host side, for the dropout seed */

@@ -358,9 +358,16 @@ int32_t check_desc(const skl_ctx *ctx, const skl_dense_desc *b) {
     SKL_CHECK(b->norm <= SKL_NORM_BATCH, SKL_ERR_INVALID_CONFIGURATION);
     SKL_CHECK(b->act <= SKL_ACT_MISH, SKL_ERR_INVALID_CONFIGURATION);
     SKL_CHECK(b->regularisation <= SKL_REGU_L2, SKL_ERR_INVALID_CONFIGURATION);
-    // check_tile_dim (device.rs:248-258)
-    SKL_CHECK(!(b->dtype == SKL_F16 && ctx->tile_dim != 16), SKL_ERR_HARDWARE_CONSTRAINT);
     SKL_CHECK(b->w, SKL_ERR_NULL_POINTER);
+    return SKL_OK;
+}
+
+// check_tile_dim (device.rs:248-258).  The reference runs it in gpu_forward_pass
+// (ffn_device.rs:20) and gpu_hidden_layer_backward_pass (ffn_device.rs:369) only,
+// after the DenseBlock method's own checks; the same calls here check it at the
+// same point, and the output error and output-layer backward do not.
+int32_t check_tile(const skl_ctx *ctx, const skl_dense_desc *b) {
+    SKL_CHECK(!(b->dtype == SKL_F16 && ctx->tile_dim != 16), SKL_ERR_HARDWARE_CONSTRAINT);
     return SKL_OK;
 }
 
@@ -561,7 +568,8 @@ int32_t skl_fill(skl_ctx *ctx, void *dst, uint32_t dtype, float v, size_t n) {
 int32_t skl_cast(skl_ctx *ctx, const void *src, uint32_t sdt, void *dst, uint32_t ddt, size_t n) {
     int32_t r = enter(ctx);
     if (r) return r;
-    if (sdt > SKL_F16 || ddt > SKL_F16) return SKL_ERR_UNSUPPORTED_CAST;
+    // gpu_cast_t (util_device.rs:23-32) knows f32 -> f16 and f16 -> f32 only
+    if (sdt > SKL_F16 || ddt > SKL_F16 || sdt == ddt) return SKL_ERR_UNSUPPORTED_CAST;
     if (n && (!src || !dst)) return SKL_ERR_NULL_POINTER;
     SKL_TRY(launch_cast(src, sdt, dst, ddt, n, ctx->stream));
     return finish(ctx);
@@ -578,8 +586,9 @@ int32_t skl_dense_forward(skl_ctx *ctx, const skl_dense_desc *b, const void *in,
     int32_t r = enter(ctx);
     if (r) return r;
     if ((r = check_desc(ctx, b))) return r;
-    if ((r = check_input(b, in, in_rows, in_cols, batch))) return r;
-    if ((r = check_act_batch(b, batch))) return r;
+    if ((r = check_input(b, in, in_rows, in_cols, batch))) return r;   // mlp.rs:549
+    if ((r = check_act_batch(b, batch))) return r;                    // mlp.rs:551-568
+    if ((r = check_tile(ctx, b))) return r;                           // ffn_device.rs:20
     if ((r = check_norm_cache(b))) return r;
     SKL_CHECK(b->out && b->predrop && b->preact, SKL_ERR_NULL_POINTER);
     const bool use_bias = b->norm != SKL_NORM_BATCH;   // ffn_device.rs:30
@@ -704,6 +713,7 @@ static int32_t hidden_error_impl(skl_ctx *ctx, const skl_dense_desc *cur, const 
     SKL_CHECK(batch <= cur->max_batch, SKL_ERR_ALLOCATION_LIMIT);
     SKL_CHECK(next->max_batch >= batch, SKL_ERR_MISMATCHED_DIMENSIONS);          // mlp.rs:699-706
     if ((r = check_act_batch(cur, batch))) return r;
+    if ((r = check_tile(ctx, cur))) return r;                                    // ffn_device.rs:369
     if ((r = check_backward_buffers(cur))) return r;
     SKL_CHECK(cur->predrop && cur->preact && cur->mask, SKL_ERR_NULL_POINTER);
     SKL_CHECK(next->d_prenorm, SKL_ERR_NULL_POINTER);
@@ -903,8 +913,13 @@ int32_t skl_dense_backward_hidden(skl_ctx *ctx, const skl_dense_desc *cur, const
     if (r) return r;
     SKL_CHECK(t, SKL_ERR_NULL_POINTER);
     if ((r = check_desc(ctx, cur))) return r;
+    if ((r = check_desc(ctx, next))) return r;
+    // backward_hidden (mlp.rs:682-726), in its order
     SKL_CHECK(cur->is_training, SKL_ERR_TRAINING_MODE_REQUIRED);
     if ((r = check_input(cur, in, in_rows, in_cols, t->batch_size))) return r;
+    SKL_CHECK(next->inputs == cur->outputs, SKL_ERR_MISMATCHED_DIMENSIONS);      // mlp.rs:690-697
+    SKL_CHECK(next->max_batch >= in_rows, SKL_ERR_MISMATCHED_DIMENSIONS);        // mlp.rs:699-706
+    if ((r = check_act_batch(cur, t->batch_size))) return r;                     // mlp.rs:708-726
     if ((r = hidden_error_impl(ctx, cur, next, t->batch_size))) return r;
     if ((r = backward_impl(ctx, cur, in, in_rows, in_cols, t, step))) return r;
     return finish(ctx);

@@ -56,12 +56,8 @@ hipError_t launch_cast(const void *src, uint32_t sdt, void *dst, uint32_t ddt, s
     else if (sdt == 1 && ddt == 0)
         hipLaunchKernelGGL((cast_kernel<half_t, float>), grid_for(n, 256), dim3(256), 0, s, (const half_t *)src,
                            (float *)dst, (uint64_t)n);
-    else if (sdt == 0 && ddt == 0)
-        hipLaunchKernelGGL((cast_kernel<float, float>), grid_for(n, 256), dim3(256), 0, s, (const float *)src,
-                           (float *)dst, (uint64_t)n);
     else
-        hipLaunchKernelGGL((cast_kernel<half_t, half_t>), grid_for(n, 256), dim3(256), 0, s, (const half_t *)src,
-                           (half_t *)dst, (uint64_t)n);
+        return hipErrorInvalidValue;   // the C ABI admits f32 <-> f16 only
     return hipGetLastError();
 }
 

@@ -14,6 +14,14 @@
 //                                             DIR/spec.txt on DIR/x.bin, DIR/t.bin (needs a GPU);
 //                                             then saves DIR/net.safetensors, loads it back and
 //                                             checks the reloaded network
+//   soklyn_tool convert DIR K N BATCH SEED    DenseBlock<f32>::convert_f16, one fp16 Adam step
+//                                             (MSE on DIR/x.bin, DIR/t.bin), convert_f32, one fp32
+//                                             forward; dumps every stage into DIR (needs a GPU)
+//   soklyn_tool sched cosine MIN MAX TOTAL WARMUP N | sched exp LR FACTOR N |
+//              sched plateau PATIENCE min|max FACTOR MIN_LR RESET_LR V...
+//                                             learning-rate schedules (no GPU): the rate after
+//                                             construction (plateau: after reset) and after each
+//                                             step, as f32 bit patterns (hex)
 //   soklyn_tool st-demo FILE                  write a synthetic safetensors file (no GPU)
 //   soklyn_tool st-dump FILE                  print a safetensors file: metadata, then per tensor
 //                                             name, dtype, shape and the bytes in hex (no GPU)
@@ -37,6 +45,7 @@
 #include <vector>
 
 #include "safetensors.hpp"
+#include "scheduler.hpp"
 #include "soklyn.hpp"
 
 using namespace soklyn;
@@ -45,7 +54,7 @@ namespace {
 
 int usage() {
     std::fprintf(stderr, "usage: soklyn_tool selftest | chacha R KEYHEX CTR N | init KIND SEED FACTOR FIN FOUT LEN | "
-                         "ids | train DIR\n");
+                         "ids | train DIR | convert DIR K N BATCH SEED | sched ... | st-demo FILE | st-dump FILE\n");
     return 2;
 }
 
@@ -365,6 +374,112 @@ template <class T> int train(const std::string &dir, const std::map<std::string,
     return 0;
 }
 
+// ---- sched: learning-rate schedules (scheduler.rs) -------------------------------------------
+void print_bits(float v, bool last) {
+    uint32_t x;
+    std::memcpy(&x, &v, 4);
+    std::printf("%08x%c", x, last ? '\n' : ' ');
+}
+
+int sched(int argc, char **argv) {
+    const std::string kind = argv[2];
+    if (kind == "cosine" && argc == 8) {
+        CosineDecayLR s(std::strtof(argv[3], nullptr), std::strtof(argv[4], nullptr), std::strtoul(argv[5], nullptr, 10),
+                        std::strtoul(argv[6], nullptr, 10));
+        const size_t n = std::strtoul(argv[7], nullptr, 10);
+        print_bits(s.get_learning_rate(), n == 0);
+        for (size_t i = 0; i < n; ++i) print_bits(s.step(), i + 1 == n);
+        s.reset();
+        std::printf("reset ");
+        print_bits(s.get_learning_rate(), true);
+        return 0;
+    }
+    if (kind == "exp" && argc == 6) {
+        ExponentialLR s(std::strtof(argv[3], nullptr), std::strtof(argv[4], nullptr));
+        const size_t n = std::strtoul(argv[5], nullptr, 10);
+        print_bits(s.get_learning_rate(), n == 0);
+        for (size_t i = 0; i < n; ++i) print_bits(s.step(), i + 1 == n);
+        s.reset();
+        std::printf("reset ");
+        print_bits(s.get_learning_rate(), true);
+        return 0;
+    }
+    if (kind == "plateau" && argc >= 8) {
+        const std::string mode = argv[4];
+        ReduceLROnPlateauScheduler s(std::strtoul(argv[3], nullptr, 10),
+                                     mode == "max" ? SchedulerMode::Maximize : SchedulerMode::Minimize,
+                                     std::strtof(argv[5], nullptr), std::strtof(argv[6], nullptr));
+        print_bits(s.get_learning_rate(), false);
+        s.reset(std::strtof(argv[7], nullptr));
+        print_bits(s.get_learning_rate(), argc == 8);
+        for (int i = 8; i < argc; ++i) print_bits(s.step(std::strtof(argv[i], nullptr)), i + 1 == argc);
+        return 0;
+    }
+    return usage();
+}
+
+// ---- convert: DenseBlock<f32>::convert_f16 -> one training step -> convert_f32 ---------------
+// (mlp.rs:835-888).  One RMSNorm + SiLU block K -> N, He-normal init from init_seed; x
+// [batch x K] and the MSE target t [batch x N] are read from dir.  Dumps every stage so the
+// caller can check the casts bit for bit and the step against the oracle.
+int convert(const std::string &dir, size_t K, size_t N, size_t batch, uint64_t init_seed) {
+    GpuContext ctx;
+    InitHeNormalFunc init(init_seed, 1.0f);
+    LayerInitConfig cfg;
+    cfg.normalisation = Normalisation::RMSNorm;
+    cfg.activation = Activation::silu();
+    DenseBlock<float> b32 = DenseBlock<float>::new_with_config(ctx, true, K, N, batch, init, cfg);
+    write_f32(dir + "/w32_init.bin", host_f32(ctx, b32.get_weights()));
+    write_f32(dir + "/mask32_init.bin", host_f32(ctx, b32.get_masks()));
+
+    DenseBlock<f16> b16 = std::move(b32).convert_f16(ctx);
+    write_f32(dir + "/w16.bin", host_f32(ctx, b16.get_weights()));
+    write_f32(dir + "/master_w16.bin", host_f32(ctx, b16.get_master_weights().value()));
+    write_f32(dir + "/master_norm_w16.bin", host_f32(ctx, b16.get_master_norm_weights().value()));
+    write_f32(dir + "/norm_w16.bin", host_f32(ctx, b16.get_norm_weights()));
+    write_f32(dir + "/mask16.bin", host_f32(ctx, b16.get_masks()));
+
+    auto to_h = [](const std::vector<float> &f) {
+        std::vector<f16> v(f.size());
+        for (size_t i = 0; i < f.size(); ++i) v[i] = PrecisionType<f16>::from_f32(f[i]);
+        return v;
+    };
+    const Tensor2D<f16> x = Tensor2D<f16>::from_cpu_vector(ctx, to_h(read_f32(dir + "/x.bin", batch * K)), {batch, K});
+    const Tensor2D<f16> t = Tensor2D<f16>::from_cpu_vector(ctx, to_h(read_f32(dir + "/t.bin", batch * N)), {batch, N});
+    const Optimiser adam = Optimiser::adam(0.9f, 0.999f, 1e-8f);
+    const TrainContext tc{&adam, &adam, batch, 1e-3f, FLT_MAX};
+    b16.forward(ctx, x, batch, false, 1);
+    b16.compute_loss(ctx, t, LossConfig{LossFunc::MeanSquareLoss, Activation::identity()});
+    b16.backward_output(ctx, x, tc, 1);
+    ctx.synchronize();
+    write_f32(dir + "/out16.bin", host_f32(ctx, b16.get_outputs()));
+    write_f32(dir + "/d_prenorm16.bin", host_f32(ctx, b16.get_delta_prenorm_out()));
+    write_f32(dir + "/w16_step.bin", host_f32(ctx, b16.get_weights()));
+    write_f32(dir + "/master_w16_step.bin", host_f32(ctx, b16.get_master_weights().value()));
+    write_f32(dir + "/master_norm_w16_step.bin", host_f32(ctx, b16.get_master_norm_weights().value()));
+    write_f32(dir + "/master_b16_step.bin", host_f32(ctx, b16.get_master_biases().value()));
+    write_f32(dir + "/master_norm_b16_step.bin", host_f32(ctx, b16.get_master_norm_biases().value()));
+    write_f32(dir + "/dm_w16_step.bin", host_f32(ctx, b16.get_dm_weights()));
+    write_f32(dir + "/dv_w16_step.bin", host_f32(ctx, b16.get_dv_weights()));
+
+    DenseBlock<float> back = std::move(b16).convert_f32(ctx);
+    write_f32(dir + "/w32_back.bin", host_f32(ctx, back.get_weights()));
+    write_f32(dir + "/b32_back.bin", host_f32(ctx, back.get_biases()));
+    write_f32(dir + "/norm_w32_back.bin", host_f32(ctx, back.get_norm_weights()));
+    write_f32(dir + "/norm_b32_back.bin", host_f32(ctx, back.get_norm_biases()));
+    write_f32(dir + "/dm_w32_back.bin", host_f32(ctx, back.get_dm_weights()));
+    write_f32(dir + "/dv_w32_back.bin", host_f32(ctx, back.get_dv_weights()));
+    write_f32(dir + "/out32_back.bin", host_f32(ctx, back.get_outputs()));
+    // the converted block keeps working in fp32: one forward on the fp16 inputs
+    const std::vector<float> xf = read_f32(dir + "/x.bin", batch * K);
+    std::vector<float> xr(xf.size());
+    for (size_t i = 0; i < xf.size(); ++i) xr[i] = PrecisionType<f16>::to_f32(PrecisionType<f16>::from_f32(xf[i]));
+    const Tensor2D<float> x32 = Tensor2D<float>::from_cpu_vector(ctx, xr, {batch, K});
+    write_f32(dir + "/out32_fwd.bin", host_f32(ctx, back.forward(ctx, x32, batch, false, 2)));
+    std::printf("convert round trip done\n");
+    return 0;
+}
+
 }  // namespace
 
 int main(int argc, char **argv) {
@@ -383,6 +498,10 @@ int main(int argc, char **argv) {
         if (cmd == "ids") return ids();
         if (cmd == "st-demo" && argc == 3) return st_demo(argv[2]);
         if (cmd == "st-dump" && argc == 3) return st_dump(argv[2]);
+        if (cmd == "sched" && argc >= 3) return sched(argc, argv);
+        if (cmd == "convert" && argc == 7)
+            return convert(argv[2], std::strtoul(argv[3], nullptr, 10), std::strtoul(argv[4], nullptr, 10),
+                           std::strtoul(argv[5], nullptr, 10), std::strtoull(argv[6], nullptr, 10));
         if (cmd == "train" && argc == 3) {
             const auto spec = read_spec(std::string(argv[2]) + "/spec.txt");
             return spec.at("dtype") == "f16" ? train<f16>(argv[2], spec) : train<float>(argv[2], spec);

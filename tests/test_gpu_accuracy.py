@@ -1,0 +1,63 @@
+"""fp32 GEMM outputs against exact arithmetic, element by element.
+
+The oracle restates the reference's sequential fp32 sums (math.cu:8-50 forward,
+backward.cu:72-77 dX, backward.cu:181-186 dW); the device sums in MFMA tiles.
+Neither order is exact, so instead of gating device-vs-oracle elementwise at the
+reference order's own noise level, this checks each against float64: the device
+must be as close to the exact result as the reference's order is, within a
+factor of 2 (the metric is a maximum over millions of elements, so the two
+orders' maxima scatter around each other), and within 1e-5 normwise of it.  Shapes: config 2 at full size and the odd shapes of the parity
+tests.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from soklyn_amd import abi
+from soklyn_amd.devblock import DeviceBlock
+from tests.helpers import elementwise, he_normal, normwise, rng
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(4096, 1024, 1024), (2048, 256, 2048), (4100, 2048, 10), (1000, 777, 1531), (130, 40, 3001)]
+
+
+def judge(name, dev, orc, exact):
+    e_dev, e_orc = elementwise(dev, exact), elementwise(orc, exact)
+    n_dev = normwise(dev, exact)
+    print(f"  {name}: elementwise vs exact: device {e_dev:.2e}, reference order {e_orc:.2e}; "
+          f"device normwise vs exact {n_dev:.2e}", flush=True)
+    assert e_dev <= 2.0 * e_orc + 1e-5, f"{name}: device {e_dev:.3e} vs reference order {e_orc:.3e}"
+    assert n_dev <= 1e-5, f"{name}: normwise {n_dev:.3e}"
+
+
+@pytest.mark.parametrize("M,K,N", SHAPES)
+def test_fp32_gemms_as_accurate_as_reference_order(ctx, M, K, N):
+    g = rng(M + 3 * K + 7 * N)
+    w = he_normal(g, K, N)
+    b = (g.standard_normal((1, N)) * 0.01).astype(np.float32)
+    x = g.standard_normal((M, K)).astype(np.float32)
+    s = g.standard_normal((M, N)).astype(np.float32) * 512
+    ob = O.OracleBlock(K, N, M, w, act=abi.ACT_IDENTITY, b=b)
+    db = DeviceBlock(ctx, K, N, M, w, act=abi.ACT_IDENTITY, b=b)
+    xd = torch.from_numpy(x).cuda()
+    # forward: preact = X.W + b
+    ob.forward(x, M)
+    db.forward(xd, M)
+    exact = x.astype(np.float64) @ w.astype(np.float64) + b.astype(np.float64)
+    judge("forward preact", db.get("preact"), ob.preact, exact)
+    # error from a given sum (identity: d_prenorm = s exactly on both sides), then dX and dW
+    ob.error_from_sum(s, M)
+    db.error_from_sum(torch.from_numpy(s).cuda(), M)
+    assert np.array_equal(db.get("d_prenorm"), ob.d_prenorm)
+    dp = ob.d_prenorm.astype(np.float64)
+    dx = db.input_grad(M).cpu().numpy()
+    judge("dX", dx, ob.input_grad(M), dp @ w.astype(np.float64).T)
+    ob.backward(x, O.Optimiser.sgd(0.0), O.Optimiser.sgd(0.0), M, 0.01, 3.4e38, 1)
+    db.backward(xd, abi.train_ctx(abi.sgd(0.0), abi.sgd(0.0), M, 0.01), 1)
+    torch.cuda.synchronize()
+    # SGD from zero momentum: dv_w = dW / 512 / m
+    judge("dW (dv_w)", db.get("dv_w"), ob.dv_w, (x.astype(np.float64).T @ dp) / 512.0 / M)

@@ -11,7 +11,8 @@ the GPU box's host cores).
 
 Single blocks take one step of forward -> act' of a supplied upstream gradient ->
 dW + optimiser -> dX (bench.py's step); the MLPs take FeedForwardNetwork's step.
-Gates as everywhere: fp32 1e-4 elementwise, fp16 2e-2 normwise; dropout masks bit-exact.
+Gates as everywhere (tests/helpers.py): fp32 1e-4 normwise and 1e-2 elementwise, fp16 2e-2 normwise; dropout
+masks bit-exact.
 
 Each stage is checked on identical inputs: after the forward has been compared, the
 device's forward caches are copied into the oracle blocks before the backward.  At
@@ -28,7 +29,7 @@ import torch
 from oracle import oracle as O
 from soklyn_amd import abi
 from soklyn_amd.devblock import DeviceBlock
-from tests.helpers import FP16_TOL, FP32_TOL, check, f16, he_normal, rng
+from tests.helpers import FP16_TOL, FP32_TOL, check, check_adam_update, f16, he_normal, rng
 from tests.test_gpu_ffn import build_net
 
 pytestmark = pytest.mark.gpu
@@ -72,13 +73,13 @@ def single_block_step(ctx, M, K, N, half, act, opt_o, opt_d, lr):
     db.backward(xd, abi.train_ctx(opt_d, opt_d, M, lr), 1)
     dx = db.input_grad(M)
     torch.cuda.synchronize()
-    return ob, db, dx.cpu().numpy(), dx_ref
+    return ob, db, dx.cpu().numpy(), dx_ref, w
 
 
 def test_c2_fp32_full_size(ctx):
     tol = FP32_TOL
-    ob, db, dx, dx_ref = single_block_step(ctx, 4096, 1024, 1024, False, abi.ACT_RELU, O.Optimiser.sgd(0.0),
-                                           abi.sgd(0.0), 1e-2)
+    ob, db, dx, dx_ref, _ = single_block_step(ctx, 4096, 1024, 1024, False, abi.ACT_RELU, O.Optimiser.sgd(0.0),
+                                              abi.sgd(0.0), 1e-2)
     for n in ("grad", "d_prenorm", "dv_w", "dv_b", "w", "b"):
         check(n, db.get(n), getattr(ob, n), tol)
     check("dX", dx, dx_ref, tol)
@@ -86,10 +87,13 @@ def test_c2_fp32_full_size(ctx):
 
 def test_c3_fp16_full_size(ctx):
     tol = FP16_TOL
-    ob, db, dx, dx_ref = single_block_step(ctx, 8192, 4096, 4096, True, abi.ACT_SILU, O.Optimiser.adam(),
-                                           abi.adam(), 1e-3)
+    ob, db, dx, dx_ref, w0 = single_block_step(ctx, 8192, 4096, 4096, True, abi.ACT_SILU, O.Optimiser.adam(),
+                                               abi.adam(), 1e-3)
     for n in ("grad", "d_prenorm", "dm_w", "dv_w", "master_w", "dm_b", "master_b"):
         check(n, db.get(n), getattr(ob, n), tol)
+    # master_w moves by ~1e-3 against |w| ~ 0.1: its normwise check cannot see the update
+    check_adam_update("master_w update", w0, db.get("master_w"), db.get("dm_w"), db.get("dv_w"), 1e-3, 1,
+                      ob.master_w - w0, ob.dm_w)
     check("dX", dx, dx_ref, tol)
     # the fp16 working copy is the RNE of the fp32 master after the update
     assert np.array_equal(db.get("w"), f16(db.get("master_w")))

@@ -18,7 +18,7 @@ import pytest
 
 from oracle import oracle as O
 from soklyn_amd import abi
-from tests.helpers import FP16_TOL, FP32_TOL, check, f16, rng
+from tests.helpers import FP16_TOL, FP32_TOL, check, check_adam_update, f16, rng
 from tests.test_gpu_ffn import oracle_step
 from tests.test_safetensors_cpu import serde_pretty_header
 
@@ -154,3 +154,61 @@ def test_ffn_fp16_rms_mish_dropout_adam_two_steps(tmp_path):
         seeds = [O.scramble_seed(step, i) for i in ids]
         oracle_step(obs, x, t, M, abi.LOSS_CE, abi.ACT_SOFTMAX, O.Optimiser.adam(), 1e-3, step, True, seeds)
     compare(obs, res, FP16_TOL, True, masks=True)
+
+
+def test_convert_f16_train_convert_f32_round_trip(tmp_path):
+    """DenseBlock<f32>::convert_f16 (mlp.rs:835-856, ParamState::cast_f16 at mlp.rs:204-219), one fp16
+    Adam step, DenseBlock<f16>::convert_f32 (mlp.rs:868-888, cast_f32 at mlp.rs:186-202), one fp32
+    forward: the casts bit for bit, the step and the final forward against the oracle."""
+    K, N, M = 96, 80, 64
+    d = str(tmp_path)
+    g = rng(301)
+    x = g.standard_normal((M, K)).astype(np.float32)
+    t = g.standard_normal((M, N)).astype(np.float32)
+    x.tofile(os.path.join(d, "x.bin"))
+    t.tofile(os.path.join(d, "t.bin"))
+    assert "convert round trip done" in tool("convert", d, K, N, M, 1234)
+
+    def ld(n, shape=None):
+        a = np.fromfile(os.path.join(d, n + ".bin"), np.float32)
+        return a.reshape(shape) if shape else a
+
+    w32 = ld("w32_init", (K, N))
+    assert w32.std() > 0 and np.all(ld("mask32_init") == 1.0)
+    # convert_f16: master = the fp32 original, w = f16(RNE) of it, norm_w = 1 in both, mask cast
+    assert np.array_equal(ld("master_w16", (K, N)), w32)
+    assert np.array_equal(ld("w16", (K, N)), f16(w32))
+    assert np.all(ld("norm_w16") == 1.0) and np.all(ld("master_norm_w16") == 1.0)
+    assert np.all(ld("mask16") == 1.0)
+
+    # the fp16 step against the oracle on the same weights (convert_f16 route: master = w32)
+    ob = O.OracleBlock(K, N, M, w32, half=True, master_w=w32, norm=abi.NORM_RMS, act=abi.ACT_SILU)
+    xh, th = f16(x), f16(t)
+    ob.forward(xh, M)
+    ob.output_error(th, abi.LOSS_MSE, abi.ACT_IDENTITY)
+    ob.backward(xh, O.Optimiser.adam(), O.Optimiser.adam(), M, 1e-3, 3.4e38, 1)
+    check("out (fp16 step)", ld("out16", (M, N)), ob.out, FP16_TOL)
+    check("d_prenorm (fp16 step)", ld("d_prenorm16", (M, N)), ob.d_prenorm, FP16_TOL)
+    check("dm_w (fp16 step)", ld("dm_w16_step", (K, N)), ob.dm_w, FP16_TOL)
+    check("dv_w (fp16 step)", ld("dv_w16_step", (K, N)), ob.dv_w, FP16_TOL)
+    m_step = ld("master_w16_step", (K, N))
+    check_adam_update("master_w update", w32, m_step, ld("dm_w16_step", (K, N)), ld("dv_w16_step", (K, N)), 1e-3, 1,
+                      ob.master_w - w32, ob.dm_w)
+    assert np.array_equal(ld("w16_step", (K, N)), f16(m_step))
+
+    # convert_f32: w = the fp32 master, moments carried over, caches cast f16 -> f32 exactly
+    w_back = ld("w32_back", (K, N))
+    assert np.array_equal(w_back, m_step)
+    assert np.array_equal(ld("norm_w32_back"), ld("master_norm_w16_step"))
+    assert np.array_equal(ld("b32_back"), ld("master_b16_step"))
+    assert np.array_equal(ld("norm_b32_back"), ld("master_norm_b16_step"))
+    assert np.array_equal(ld("dm_w32_back", (K, N)), ld("dm_w16_step", (K, N)))
+    assert np.array_equal(ld("dv_w32_back", (K, N)), ld("dv_w16_step", (K, N)))
+    assert np.array_equal(ld("out32_back", (M, N)), ld("out16", (M, N)))
+
+    # and the converted block computes in fp32
+    o32 = O.OracleBlock(K, N, M, w_back, norm=abi.NORM_RMS, act=abi.ACT_SILU, b=ld("b32_back"))
+    o32.norm_w[:] = ld("norm_w32_back").reshape(1, N)
+    o32.norm_b[:] = ld("norm_b32_back").reshape(1, N)
+    o32.forward(xh, M)
+    check("out (fp32 forward after convert_f32)", ld("out32_fwd", (M, N)), o32.out, FP32_TOL)

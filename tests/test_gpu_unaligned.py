@@ -5,7 +5,7 @@ allocation).  These take the 4-column-group path that reads aligned chunks and
 splits its stores at chunk boundaries; the column sums it leaves feed the
 backward's bias and norm-parameter update, checked through the moments.
 
-Gates as everywhere: fp32 1e-4 elementwise, fp16 2e-2 normwise against the oracle.
+Gates as everywhere: fp32 1e-4 normwise and 1e-2 elementwise, fp16 2e-2 normwise against the oracle.
 """
 from __future__ import annotations
 

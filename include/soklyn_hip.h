@@ -194,6 +194,20 @@ int32_t skl_dense_backward_hidden(skl_ctx *ctx, const skl_dense_desc *cur,
 int32_t skl_dense_error_from_sum(skl_ctx *ctx, const skl_dense_desc *blk, const float *s,
                                  uint32_t batch);
 
+/* skl_dense_error_from_sum that allocates nothing.  No counterpart in the
+ * reference: for callers that cannot call hipMalloc (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation).  Same checks
+ * and same outputs as skl_dense_error_from_sum, bit for bit; the error kernel's
+ * column partial sums go to a 16 MiB device array the library holds per GPU
+ * (looked up in skl_ctx_create) instead of the context's grown buffer.
+ * Limit: splits x 3 x outputs x 4 bytes <= 16 MiB (any batch for outputs up to
+ * ~1.39 M; otherwise SKL_ERR_ALLOCATION_LIMIT, nothing written).  Every call on
+ * one GPU shares that array: calls that overlap on one GPU (two streams or two
+ * contexts) race.  It leaves no column sums behind, so a following
+ * skl_dense_backward reads d_prenorm / dNorm again (same results). */
+int32_t skl_dense_error_from_sum_noalloc(skl_ctx *ctx, const skl_dense_desc *blk, const float *s,
+                                         uint32_t batch);
+
 /* The GEMM of compute_hidden_layer_error (backward.cu:72-77) with no consumer
  * epilogue: dx[batch x inputs] fp32 = d_prenorm . W_master^T — the gradient sum
  * the layer below this block would receive (fp16 blocks: f16 operands, fp32

@@ -83,6 +83,7 @@ _SIGS = {
     "skl_dense_backward_hidden": (C.c_int32, [_VP, C.POINTER(SklDenseDesc), C.POINTER(SklDenseDesc), _VP,
                                               C.c_uint32, C.c_uint32, C.POINTER(SklTrainCtx), C.c_uint32]),
     "skl_dense_error_from_sum": (C.c_int32, [_VP, C.POINTER(SklDenseDesc), _VP, C.c_uint32]),
+    "skl_dense_error_from_sum_noalloc": (C.c_int32, [_VP, C.POINTER(SklDenseDesc), _VP, C.c_uint32]),
     "skl_dense_input_grad": (C.c_int32, [_VP, C.POINTER(SklDenseDesc), C.c_uint32, _VP]),
 }
 

@@ -8,6 +8,8 @@
 #include <math.h>
 #include <string.h>
 
+#include <mutex>
+
 #include <hip/hip_runtime.h>
 
 #include "../../include/soklyn_hip.h"
@@ -41,7 +43,17 @@ struct skl_ctx {
     size_t cols_bytes;
     ColSums cs;
     hipEvent_t gemm_start, gemm_stop;   // skl_ctx_time_next_gemm
+    void *scratch;       // device address of this device's copy of `scratch` (below)
 };
+
+// Scratch of the allocation-free entry point (skl_dense_error_from_sum_noalloc):
+// the error kernel's column partial sums [splits x 3 x n] fp32 go here instead
+// of the context's grown buffer.  One copy per GPU, allocated with the code
+// object and held until the process ends.  Host code never uses the array's
+// name as an address: skl_ctx_create looks up each device's copy once with
+// hipGetSymbolAddress and every launch takes that pointer.
+constexpr size_t NOALLOC_SCRATCH_BYTES = size_t(16) << 20;
+static __device__ __align__(256) char scratch[NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -85,6 +97,26 @@ int32_t ensure_buf(skl_ctx *ctx, void **buf, size_t *have, size_t bytes) {
 }
 
 int32_t ensure_ws(skl_ctx *ctx, size_t bytes) { return ensure_buf(ctx, &ctx->ws, &ctx->ws_bytes, bytes); }
+
+// Device address of `scratch` on device `dev` (current), looked up once per device.
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[MAX_DEVICES];
+
+int32_t scratch_address(int dev, void **out) {
+    *out = nullptr;
+    if (dev < 0 || dev >= MAX_DEVICES) return SKL_ERR_NO_DEVICE;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_status(e);
+        if (!p) return SKL_ERR_NULL_POINTER;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return SKL_OK;
+}
 
 // Room for the column sums of an error call over [rows x n]; returns the splits.
 int32_t ensure_cols(skl_ctx *ctx, uint32_t rows, uint32_t n, uint32_t *splits) {
@@ -442,7 +474,7 @@ const char *skl_status_string(int32_t s) {
     case SKL_OK: return "ok";
     case SKL_ERR_INVALID_CONFIGURATION: return "invalid configuration";
     case SKL_ERR_TRAINING_MODE_REQUIRED: return "training mode required";
-    case SKL_ERR_ALLOCATION_LIMIT: return "allocation limit exceeded";
+    case SKL_ERR_ALLOCATION_LIMIT: return "allocation limit exceeded (batch, or an allocation-free call's scratch)";
     case SKL_ERR_MISMATCHED_DIMENSIONS: return "mismatched dimensions";
     case SKL_ERR_INVALID_BATCH_SIZE: return "invalid batch size";
     case SKL_ERR_HARDWARE_CONSTRAINT: return "hardware constraint violation (fp16 requires tile_dim 16)";
@@ -467,6 +499,13 @@ int32_t skl_ctx_create(int32_t ordinal, uint32_t tile_dim, skl_ctx **out) {
     c->sync = 1;
     c->ws = nullptr;
     c->ws_bytes = 0;
+    {
+        const int32_t sr = scratch_address(ordinal, &c->scratch);
+        if (sr != SKL_OK) {
+            delete c;
+            return sr;
+        }
+    }
     // blocking w.r.t. the legacy null stream, so callers on stream 0 stay ordered
     hipError_t e = hipStreamCreateWithFlags(&c->own_stream, hipStreamDefault);
     if (e != hipSuccess) {
@@ -925,9 +964,9 @@ int32_t skl_dense_backward_hidden(skl_ctx *ctx, const skl_dense_desc *cur, const
     return finish(ctx);
 }
 
-int32_t skl_dense_error_from_sum(skl_ctx *ctx, const skl_dense_desc *b, const float *s, uint32_t batch) {
-    int32_t r = enter(ctx);
-    if (r) return r;
+// skl_dense_error_from_sum's checks, in order, and its kernel arguments
+static int32_t error_from_sum_checks(skl_ctx *ctx, const skl_dense_desc *b, const float *s, uint32_t batch) {
+    int32_t r;
     if ((r = check_desc(ctx, b))) return r;
     SKL_CHECK(b->is_training, SKL_ERR_TRAINING_MODE_REQUIRED);
     SKL_CHECK(s, SKL_ERR_NULL_POINTER);
@@ -936,7 +975,10 @@ int32_t skl_dense_error_from_sum(skl_ctx *ctx, const skl_dense_desc *b, const fl
     if ((r = check_backward_buffers(b))) return r;
     SKL_CHECK(b->predrop && b->preact && b->mask, SKL_ERR_NULL_POINTER);
     if (b->dtype == SKL_F16 && b->norm) SKL_CHECK(b->master_norm_w, SKL_ERR_NULL_POINTER);
-    if ((r = zero_dnorm_tail(ctx, b, batch))) return r;
+    return SKL_OK;
+}
+
+static ErrArgs error_from_sum_args(const skl_dense_desc *b, const float *s, uint32_t batch) {
     ErrArgs a{};
     a.dtype = b->dtype;
     a.rows = batch;
@@ -960,10 +1002,36 @@ int32_t skl_dense_error_from_sum(skl_ctx *ctx, const skl_dense_desc *b, const fl
     a.d_norm_w = b->d_norm_w;
     a.d_norm_b = b->d_norm_b;
     a.d_prenorm_h = b->dtype == SKL_F16 ? reinterpret_cast<half_t *>(b->d_prenorm_h) : nullptr;
+    return a;
+}
+
+int32_t skl_dense_error_from_sum(skl_ctx *ctx, const skl_dense_desc *b, const float *s, uint32_t batch) {
+    int32_t r = enter(ctx);
+    if (r) return r;
+    if ((r = error_from_sum_checks(ctx, b, s, batch))) return r;
+    if ((r = zero_dnorm_tail(ctx, b, batch))) return r;
+    const ErrArgs a = error_from_sum_args(b, s, batch);
     uint32_t splits = 0;
     if ((r = ensure_cols(ctx, batch, b->outputs, &splits))) return r;
     SKL_TRY(launch_error_from_sum(a, ctx->cols, splits, ctx->stream));
     record_cols(ctx, b, batch, splits);
+    return finish(ctx);
+}
+
+int32_t skl_dense_error_from_sum_noalloc(skl_ctx *ctx, const skl_dense_desc *b, const float *s, uint32_t batch) {
+    int32_t r = enter(ctx);
+    if (r) return r;
+    if ((r = error_from_sum_checks(ctx, b, s, batch))) return r;
+    SKL_CHECK(ctx->scratch, SKL_ERR_NULL_POINTER);
+    const uint32_t splits = err_col_splits(batch, b->outputs);
+    SKL_CHECK((size_t)splits * 3 * b->outputs * sizeof(float) <= NOALLOC_SCRATCH_BYTES, SKL_ERR_ALLOCATION_LIMIT);
+    if ((r = zero_dnorm_tail(ctx, b, batch))) return r;
+    const ErrArgs a = error_from_sum_args(b, s, batch);
+    // every split writes all of its partial-sum rows: nothing in the scratch needs clearing
+    SKL_TRY(launch_error_from_sum(a, reinterpret_cast<float *>(ctx->scratch), splits, ctx->stream));
+    // the partials sit in memory every call on this GPU shares: skl_dense_backward
+    // must not take them for its column sums, it reads d_prenorm / dNorm again
+    ctx->cs.valid = false;
     return finish(ctx);
 }
 

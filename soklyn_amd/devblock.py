@@ -111,6 +111,11 @@ class DeviceBlock:
         assert s.dtype == torch.float32 and s.is_contiguous()
         abi.call("skl_dense_error_from_sum", self.ctx.h, C.byref(self.desc()), C.c_void_p(s.data_ptr()), batch)
 
+    def error_from_sum_noalloc(self, s: torch.Tensor, batch: int):
+        assert s.dtype == torch.float32 and s.is_contiguous()
+        abi.call("skl_dense_error_from_sum_noalloc", self.ctx.h, C.byref(self.desc()), C.c_void_p(s.data_ptr()),
+                 batch)
+
     def input_grad(self, batch: int, out: torch.Tensor | None = None) -> torch.Tensor:
         if out is None:
             out = torch.empty((batch, self.inputs), device=self.w.device, dtype=torch.float32)

@@ -118,13 +118,18 @@ int32_t scratch_address(int dev, void **out) {
     return SKL_OK;
 }
 
+// Room for column sums of `splits` row slices over n columns.
+int32_t ensure_cols_splits(skl_ctx *ctx, uint32_t splits, uint32_t n) {
+    void *p = ctx->cols;
+    const int32_t r = ensure_buf(ctx, &p, &ctx->cols_bytes, (size_t)splits * 3 * n * sizeof(float));
+    ctx->cols = reinterpret_cast<float *>(p);
+    return r;
+}
+
 // Room for the column sums of an error call over [rows x n]; returns the splits.
 int32_t ensure_cols(skl_ctx *ctx, uint32_t rows, uint32_t n, uint32_t *splits) {
     *splits = err_col_splits(rows, n);
-    void *p = ctx->cols;
-    const int32_t r = ensure_buf(ctx, &p, &ctx->cols_bytes, (size_t)*splits * 3 * n * sizeof(float));
-    ctx->cols = reinterpret_cast<float *>(p);
-    return r;
+    return ensure_cols_splits(ctx, *splits, n);
 }
 
 void record_cols(skl_ctx *ctx, const skl_dense_desc *b, uint32_t rows, uint32_t splits) {
@@ -779,6 +784,40 @@ static int32_t hidden_error_impl(skl_ctx *ctx, const skl_dense_desc *cur, const 
     g.splits = 1;
     g.op = Op::InputGrad;
     const GemmPlan plan = plan_gemm(g);
+    ErrEpi &e = g.err;
+    // an operand act' does not read aliases the mask (loaded anyway: cache hits)
+    e.predrop = act_uses_output(cur->act) ? cur->predrop : cur->mask;
+    e.preact = act_uses_input(cur->act) ? cur->preact : cur->mask;
+    e.mask = cur->mask;
+    e.norm_rstd = cur->norm_rstd;
+    e.centered = cur->centered;
+    e.prenorm = cur->prenorm;
+    e.nw = master_norm_w(cur);
+    e.grad = cur->grad;
+    e.d_prenorm = cur->d_prenorm;
+    e.d_norm_w = cur->d_norm_w;
+    e.d_norm_b = cur->d_norm_b;
+    e.d_prenorm_h = reinterpret_cast<half_t *>(cur->d_prenorm_h);
+    e.norm = cur->norm;
+    e.act = cur->act;
+    e.ldc = cur->outputs;
+    e.ncols = cur->outputs;
+    e.leaky = cur->act == SKL_ACT_LEAKY_RELU ? cur->leaky : 0.0f;
+    e.inv_n = 1.0f / (float)cur->outputs;
+    e.inv_m = 1.0f / (float)batch;
+    if (plan.dma && hidden_err_fusable(e, batch, cur->outputs)) {
+        // One kernel, as the reference has it (backward.cu:59-102): the 256x256
+        // GEMM's epilogue computes the error from the sum in its accumulators
+        // and leaves the column sums of each 256-row tile for cur's backward.
+        const uint32_t tiles_m = plan.Mp / 256;
+        if ((r = ensure_cols_splits(ctx, tiles_m, cur->outputs))) return r;
+        if ((r = ensure_ws(ctx, plan.bytes()))) return r;
+        e.partials = ctx->cols;
+        g.op = Op::HiddenErr;
+        if ((r = exec_gemm(ctx, g, plan, reinterpret_cast<char *>(ctx->ws)))) return r;
+        record_cols(ctx, cur, batch, tiles_m);
+        return SKL_OK;
+    }
     // s on the kernel's whole (padded) grid: the full-tile epilogue, 16-byte rows
     const uint32_t s_ld = plan.Np;
     const size_t s_bytes = ((size_t)plan.Mp * s_ld * sizeof(float) + 255) & ~(size_t)255;

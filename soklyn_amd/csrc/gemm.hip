@@ -253,6 +253,97 @@ template <typename T> struct EpiOptK {
     }
 };
 
+// ---- hidden-layer error from the dX sum (fused) -----------------------------------
+// compute_hidden_layer_error_kernel's epilogue (backward.cu:79-100) on the sum in
+// the accumulators: e = mask * act'(s, predrop, preact); grad = e; the element-
+// local norm gradient (util.cu:175-215, loss scale 1) into d_prenorm, its fp16
+// copy and dNorm; and per-thread running column sums of d_prenorm / dNorm_w /
+// dNorm_b, which flush() reduces over the 8 waves in a fixed order into the
+// tile's row of partials (the inputs of the bias / norm-parameter update).
+template <typename T> struct EpiErrK {
+    typedef ErrEpi Params;
+    static constexpr bool kColSums = true;
+    __device__ __forceinline__ static uint32_t ldc(const ErrEpi &e) { return e.ldc; }
+    __device__ __forceinline__ static ErrEpi at_split(const ErrEpi &e, uint32_t) { return e; }
+    // per-column operands of 4 columns: the norm weight, and BatchNorm's per-column rstd
+    struct Col { f32x4 nw, rstd; };
+    // per-element operands of one row's 4 columns, as loaded (T)
+    struct Pre { f16x4 pd, pa, mk, pn; float rstd; };
+    // running sums of the thread's 4 columns
+    struct Acc { f32x4 dp, nw, nb; };
+    __device__ __forceinline__ static Col column(const ErrEpi &e, uint32_t n) {
+        Col c;
+        c.nw = e.norm ? load4<float>(e.nw, n) : f32x4{0, 0, 0, 0};
+        c.rstd = e.norm == 3 ? load4<T>(e.norm_rstd, n) : f32x4{0, 0, 0, 0};
+        return c;
+    }
+    __device__ __forceinline__ static f16x4 ld4h(const void *p, uint64_t idx) {
+        return *reinterpret_cast<const f16x4 *>(reinterpret_cast<const half_t *>(p) + idx);
+    }
+    __device__ __forceinline__ static void load(const ErrEpi &e, uint64_t idx, uint32_t m, Pre &q) {
+        static_assert(sizeof(T) == 2, "the 256x256 kernel is fp16");
+        q.pd = ld4h(e.predrop, idx);
+        q.pa = ld4h(e.preact, idx);
+        q.mk = ld4h(e.mask, idx);
+        q.pn = e.norm ? ld4h(e.norm == 1 ? e.prenorm : e.centered, idx) : f16x4{0, 0, 0, 0};
+        q.rstd = (e.norm == 1 || e.norm == 2) ? to_f32(reinterpret_cast<const T *>(e.norm_rstd)[m]) : 0.0f;
+    }
+    __device__ __forceinline__ static void finish(const ErrEpi &e, uint64_t idx, uint32_t, uint32_t, floatx4 v,
+                                                  const Col &col, const Pre &q, Acc &acc) {
+        f32x4 g, dp, dnw = {0, 0, 0, 0}, dnb = {0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            g[j] = (float)q.mk[j] * activation_derivative(e.act, v[j], (float)q.pd[j], (float)q.pa[j], e.leaky);
+            dp[j] = g[j];
+            if (e.norm) {
+                const float p = (float)q.pn[j];
+                const NormGrad ng = norm_grad(e.norm, g[j], p, p, e.norm == 3 ? col.rstd[j] : q.rstd, col.nw[j],
+                                              e.inv_n, e.inv_m);
+                dp[j] = ng.d_prenorm;
+                dnw[j] = ng.dnw;
+                dnb[j] = ng.dnb;
+            }
+        }
+        __builtin_nontemporal_store(g, reinterpret_cast<f32x4 *>(e.grad + idx));
+        *reinterpret_cast<f32x4 *>(e.d_prenorm + idx) = dp;
+        *reinterpret_cast<f16x4 *>(e.d_prenorm_h + idx) = f16x4{(half_t)dp[0], (half_t)dp[1], (half_t)dp[2],
+                                                                (half_t)dp[3]};
+        if (e.norm) {
+            __builtin_nontemporal_store(dnw, reinterpret_cast<f32x4 *>(e.d_norm_w + idx));
+            __builtin_nontemporal_store(dnb, reinterpret_cast<f32x4 *>(e.d_norm_b + idx));
+        }
+        acc.dp += dp;
+        acc.nw += dnw;
+        acc.nb += dnb;
+    }
+    struct Col1 {};   // no element-by-element form: whole tiles only
+    // The tile's column sums: each of the NW waves leaves its 3 x 256 running sums
+    // in LDS (column 4 lane + j of the tile), then the block adds the waves in
+    // order 0..NW-1 and writes the columns < ncols of partials[tm][k].  lds:
+    // NW x 3 x 256 floats; the caller has made sure no wave still reads it.
+    template <int NW>
+    __device__ __forceinline__ static void flush(const ErrEpi &e, const Acc &acc, float *lds, uint32_t tid,
+                                                 uint32_t tm, uint32_t n0) {
+        const uint32_t lane = tid & 63u, wave = tid >> 6;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t c = 4u * lane + j;
+            lds[(wave * 3 + 0) * 256 + c] = acc.dp[j];
+            lds[(wave * 3 + 1) * 256 + c] = acc.nw[j];
+            lds[(wave * 3 + 2) * 256 + c] = acc.nb[j];
+        }
+        __syncthreads();
+        for (uint32_t t = tid; t < 3 * 256; t += 64 * NW) {
+            const uint32_t k = t >> 8, c = t & 255u;
+            if ((k > 0 && !e.norm) || n0 + c >= e.ncols) continue;
+            float s = 0.0f;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) s += lds[(w * 3 + k) * 256 + c];
+            e.partials[((uint64_t)tm * 3 + k) * e.ncols + n0 + c] = s;
+        }
+    }
+};
+
 // ---- tile configurations ----------------------------------------------------------
 template <typename T, int BM, int BN, int BK, int WM, int WN> struct Cfg {
     typedef T type;
@@ -320,6 +411,7 @@ template <class C> static hipError_t dispatch_op(const GemmLaunch &g, hipStream_
     case Op::DwOpt:
         return g.a_kcontig ? dispatch_vec<C, true, true, EpiOptK<T>>(g, g.opt, s)
                            : dispatch_vec<C, false, false, EpiOptK<T>>(g, g.opt, s);
+    case Op::HiddenErr: break;   // the 256x256 kernel only
     }
     return hipErrorInvalidValue;
 }
@@ -333,6 +425,7 @@ template <class C> static hipError_t dispatch_kk(const GemmLaunch &g, hipStream_
     case Op::InputGrad:
     case Op::DwPartial: return dispatch_vec<C, true, true, EpiStoreK>(g, g.st, s);
     case Op::DwOpt: return dispatch_vec<C, true, true, EpiOptK<T>>(g, g.opt, s);
+    case Op::HiddenErr: break;   // the 256x256 kernel only
     }
     return hipErrorInvalidValue;
 }
@@ -377,6 +470,7 @@ static uint32_t epi_ldc(const GemmLaunch &g) {
     case Op::InputGrad:
     case Op::DwPartial: return g.st.ldc;
     case Op::DwOpt: return g.opt.ldc;
+    case Op::HiddenErr: return g.err.ldc;
     }
     return 0;
 }
@@ -391,9 +485,30 @@ bool gemm_dma_shape_ok(const GemmLaunch &g) {
     return a_rows * g.lda * 2 < (1ull << 32) && b_rows * g.ldb * 2 < (1ull << 32);
 }
 
+// The fused error epilogue's 4-column accesses need every per-element buffer
+// 16-byte aligned (fp32) / 8-byte aligned (fp16 at a multiple of 4 elements).
+static bool err_epi_aligned(const ErrEpi &e) {
+    const void *p[] = {e.predrop, e.preact, e.mask, e.grad, e.d_prenorm, e.d_prenorm_h,
+                       e.norm ? e.d_norm_w : nullptr, e.norm ? e.d_norm_b : nullptr,
+                       e.norm == 1 ? e.prenorm : nullptr, e.norm >= 2 ? e.centered : nullptr,
+                       e.norm ? e.nw : nullptr, e.norm == 3 ? e.norm_rstd : nullptr};
+    for (const void *q : p)
+        if (q && !aligned16(q)) return false;
+    return true;
+}
+
+// The hidden error of an M x N output can be fused into the 256x256 kernel:
+// whole tiles (no padded output), 4-aligned rows, aligned buffers.  Ragged
+// outputs keep the GEMM + error kernel pair: an element-by-element form of the
+// fused epilogue was measured 1.3x slower than that pair on config 5's shapes.
+bool hidden_err_fusable(const ErrEpi &e, uint32_t M, uint32_t N) {
+    return M % 256 == 0 && N % 256 == 0 && e.ldc % 4 == 0 && err_epi_aligned(e);
+}
+
 // Whole output tiles with a 4-aligned leading dimension: the batched epilogue.
 static bool dma_full_epilogue(const GemmLaunch &g) {
     const uint32_t mv = g.mv ? g.mv : g.M, nv = g.nv ? g.nv : g.N;
+    if (g.op == Op::HiddenErr && !err_epi_aligned(g.err)) return false;
     return mv == g.M && nv == g.N && epi_ldc(g) % 4 == 0;
 }
 
@@ -429,6 +544,8 @@ static hipError_t run_dma(const GemmLaunch &g, const typename Epi::Params &p, ui
     const half_t *B = reinterpret_cast<const half_t *>(g.B);
     if (dma_full_epilogue(g))
         launch_timed(g, gemm_dma_kernel<Epi, AK, BK_, NW, false, MI>, grid, dim3(64 * NW), s, sh, A, B, p);
+    else if constexpr (EpiSums<Epi>::value)
+        return hipErrorInvalidValue;   // whole tiles only (hidden_err_fusable)
     else
         launch_timed(g, gemm_dma_kernel<Epi, AK, BK_, NW, true, MI>, grid, dim3(64 * NW), s, sh, A, B, p);
     return hipGetLastError();
@@ -453,6 +570,8 @@ hipError_t launch_gemm_dma(const GemmLaunch &g, hipStream_t s) {
     case Op::DwOpt:
         return kk ? run_dma<EpiOptK<half_t>, true, true>(g, g.opt, splits, kps, s)
                   : run_dma<EpiOptK<half_t>, false, false>(g, g.opt, splits, kps, s);
+    case Op::HiddenErr:
+        return kk ? run_dma<EpiErrK<half_t>, true, true>(g, g.err, splits, kps, s) : hipErrorInvalidValue;
     }
     return hipErrorInvalidValue;
 }

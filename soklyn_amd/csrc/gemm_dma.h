@@ -57,6 +57,8 @@
 // Operand offsets are 32-bit (rows * ld * 2 bytes < 4 GiB).
 #pragma once
 
+#include <type_traits>
+
 #include "gemm.h"
 
 namespace skl {
@@ -268,6 +270,19 @@ template <int NW, int NF, int MI = 32> struct OpN {
             pin(f.v[i][1]);
         }
     }
+};
+
+// Epilogues with running column sums (EpiErrK) declare kColSums, an Acc type,
+// finish(..., Acc &) and flush<NW>(), and run on whole tiles only; the others
+// have none.
+struct NoAcc {};
+template <class E, class = void> struct EpiSums {
+    static constexpr bool value = false;
+    typedef NoAcc Acc;
+};
+template <class E> struct EpiSums<E, std::void_t<decltype(E::kColSums)>> {
+    static constexpr bool value = E::kColSums;
+    typedef typename E::Acc Acc;
 };
 
 template <bool KC, int NW, int NF, int MI> struct DmaOpSel { typedef OpK<NW, NF, MI> type; };
@@ -506,6 +521,9 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
     // instead of paying one memory latency per row (4 rows for large per-row
     // operand sets at 8 waves, whose 256-register budget they would overflow).
     constexpr int EPI_BATCH = (NW == 8 && sizeof(typename Epi::Pre) > 32) ? 4 : 8;
+    constexpr bool SUMS = EpiSums<Epi>::value;
+    static_assert(!(SUMS && EDGE), "column-sum epilogues run on whole tiles only");
+    typename EpiSums<Epi>::Acc csum{};
     constexpr int ROWS_PER_THREAD = PROWS / NW;
     static_assert(ROWS_PER_THREAD % EPI_BATCH == 0, "epilogue batch");
     static_assert(C::BN / 4 == 64, "one wave per 256-column row");
@@ -587,10 +605,19 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
             for (int u = 0; u < EPI_BATCH; ++u) {
                 const uint32_t r = wave + (uint32_t)NW * (b + u);
                 const floatx4 v = *reinterpret_cast<const floatx4 *>(E + r * EPITCH + c);
-                Epi::finish(eps, (uint64_t)mrow[u] * Epi::ldc(eps) + n0 + c, mrow[u], n0 + c, v, col, pre[u]);
+                if constexpr (SUMS)
+                    Epi::finish(eps, (uint64_t)mrow[u] * Epi::ldc(eps) + n0 + c, mrow[u], n0 + c, v, col, pre[u],
+                                csum);
+                else
+                    Epi::finish(eps, (uint64_t)mrow[u] * Epi::ldc(eps) + n0 + c, mrow[u], n0 + c, v, col, pre[u]);
             }
         }
         if (pass + 1 < C::TWM / RPP) lds_barrier();   // E is rewritten by the next pass
+    }
+    if constexpr (SUMS) {
+        static_assert(NW * 3 * 256 * 4 <= EPI_BYTES, "column-sum staging fits the epilogue's LDS");
+        lds_barrier();   // every wave is done reading E
+        Epi::template flush<NW>(eps, csum, E, tid, tm, n0);
     }
 }
 

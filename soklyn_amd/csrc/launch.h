@@ -39,7 +39,27 @@ struct StoreEpi {
     uint32_t ldc, pad;
 };
 
-enum class Op { Fwd, InputGrad, DwOpt, DwPartial };
+// Hidden-layer error fused into the dX GEMM's epilogue (backward.cu:59-102 in
+// one kernel, as the reference has it): from the sum s in the accumulators,
+// e = mask * act'(s, predrop, preact), grad = e, the element-local norm
+// gradient into d_prenorm / d_prenorm_h / dNorm, and the column sums of
+// d_prenorm / dNorm_w / dNorm_b of each 256-row tile into
+// partials[tile_m][k][ncols] (k = 0, and 1, 2 with a norm).
+struct ErrEpi {
+    const void *predrop, *preact, *mask;          // T [rows x ldc]
+    const void *norm_rstd, *centered, *prenorm;   // T
+    const float *nw;                              // master norm weight [ncols]
+    float *grad, *d_prenorm, *d_norm_w, *d_norm_b;
+    half_t *d_prenorm_h;
+    float *partials;
+    uint32_t norm, act, ldc, ncols;
+    float leaky, inv_n, inv_m, pad;
+};
+
+enum class Op { Fwd, InputGrad, DwOpt, DwPartial, HiddenErr };
+// The fused hidden error fits the 256x256 kernel's output of M x N (whole tiles,
+// 4-aligned rows, 16-byte aligned buffers).
+bool hidden_err_fusable(const ErrEpi &e, uint32_t M, uint32_t N);
 
 // One GEMM launch.  dtype selects fp16 (MFMA 32x32x16 f16) or fp32
 // (MFMA 32x32x2 f32).  a_kcontig / b_kcontig as in gemm.h.
@@ -54,6 +74,7 @@ struct GemmLaunch {
     FwdEpi fwd;
     OptEpi opt;
     StoreEpi st;
+    ErrEpi err;
     const float *b32;     // dW: fp32 d_prenorm (ld N), read by the skinny kernel instead of B
     // When set, the GEMM kernel's own dispatch records these events at its start
     // and end (hipExtLaunchKernelGGL: no marker packets between kernels).

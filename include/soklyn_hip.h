@@ -200,8 +200,10 @@ int32_t skl_dense_error_from_sum(skl_ctx *ctx, const skl_dense_desc *blk, const 
  * and same outputs as skl_dense_error_from_sum, bit for bit; the error kernel's
  * column partial sums go to a 16 MiB device array the library holds per GPU
  * (looked up in skl_ctx_create) instead of the context's grown buffer.
- * Limit: splits x 3 x outputs x 4 bytes <= 16 MiB (any batch for outputs up to
- * ~1.39 M; otherwise SKL_ERR_ALLOCATION_LIMIT, nothing written).  Every call on
+ * Limit: partial rows x 3 x outputs x 4 bytes <= 16 MiB, which holds at any
+ * batch for outputs below 466 K (outputs % 4 == 0), 233 K (outputs % 4 == 2)
+ * or 116 K (odd outputs); otherwise SKL_ERR_ALLOCATION_LIMIT, nothing
+ * written.  Every call on
  * one GPU shares that array: calls that overlap on one GPU (two streams or two
  * contexts) race.  It leaves no column sums behind, so a following
  * skl_dense_backward reads d_prenorm / dNorm again (same results). */

@@ -508,36 +508,212 @@ hipError_t launch_softmax(uint32_t dtype, void *out, uint32_t rows, uint32_t n, 
 }
 
 // ---- error kernels ------------------------------------------------------------------
-// A thread owns 4 consecutive elements of one row (cnt <= 4 of them exist).
-// VEC (n % 4 == 0, 16-byte aligned buffers): GrpV, 16-byte fp32 / 8-byte fp16
-// accesses; otherwise GrpUA below.
-template <typename T> struct GrpV {
-    __device__ __forceinline__ static f32x4 ld(const void *p, uint64_t i, uint32_t) { return load4<T>(p, i); }
-    __device__ __forceinline__ static f32x4 ldf(const float *p, uint64_t i, uint32_t, bool nt = false) {
-        return nt ? __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p + i))
-                  : *reinterpret_cast<const f32x4 *>(p + i);
+// Loss delta of one element (backward.cu:24-45).
+__device__ __forceinline__ float output_err1(const ErrArgs &a, float out, float tg, float pre) {
+    const float o = activation(a.act, out, a.leaky);
+    if (a.loss == 0) return activation_derivative(a.act, o - tg, o, pre, a.leaky);
+    if ((a.loss == 1 && a.act == 5) || (a.loss == 2 && a.act == 1)) return o - tg;
+    return 0.0f;
+}
+
+// The element-local norm gradient (util.cu:175-215) of one element with error e;
+// pc is its prenorm (RMS) or centered (LN, BN) value.  d_prenorm carries the
+// loss scale.
+struct ErrOut {
+    float dp, dnw, dnb;
+};
+__device__ __forceinline__ ErrOut err_norm1(const ErrArgs &a, float e, float pc, float rstd, float nw) {
+    ErrOut o{e, 0.0f, 0.0f};
+    if (a.norm) {
+        const NormGrad g =
+            norm_grad(a.norm, e, a.norm == 1 ? pc : 0.0f, a.norm >= 2 ? pc : 0.0f, rstd, nw, a.inv_n, a.inv_m);
+        o = ErrOut{g.d_prenorm, g.dnw, g.dnb};
     }
-    __device__ __forceinline__ static void stf(float *p, uint64_t i, f32x4 v, uint32_t, bool nt = false) {
-        if (nt)
-            __builtin_nontemporal_store(v, reinterpret_cast<f32x4 *>(p + i));
-        else
-            *reinterpret_cast<f32x4 *>(p + i) = v;
-    }
-    __device__ __forceinline__ static void sth(half_t *p, uint64_t i, f32x4 v, uint32_t) {
-        store4<half_t>(p, i, v);
-    }
+    o.dp = o.dp * a.loss_scale;
+    return o;
+}
+
+struct ErrAcc {   // running column sums of a thread's 4 elements
+    f32x4 dp, nw, nb;
 };
 
-// Rows at any alignment (n % 4 != 0, or buffers not 16-byte aligned): the group
-// of elements i .. i + cnt - 1 of an array p is read as the aligned 4-element
-// chunk holding element i plus, when the group runs into the next chunk, that
-// chunk too.  Each chunk read holds an element of the group, so no read leaves
-// the 16-byte blocks the group's own elements lie in.  Stores split the group at
-// the chunk boundary into aligned 1-, 2- and 4-element pieces.  For a row-
-// strided group (first column a multiple of 4) the offset o of element i in its
-// chunk is the same in every lane of the row, so the switches on o branch
-// uniformly; only the lane that holds a row's last, partial group (cnt < 4)
-// takes the element-by-element path.
+// Error + column sums in one pass (backward.cu:12-56 for the output layer,
+// 79-100 for a supplied sum s), on 16-byte aligned buffers: the [rows x n]
+// arrays as one flat array.  A band of B = 4 / gcd(n, 4) rows holds B n / 4
+// whole 4-element chunks; thread j owns chunk j of every band of its row
+// slice, so each load and store of a row-strided array is one 16-byte (fp32)
+// or 8-byte (fp16) access whatever n is.  Element q of the chunk lies in row
+// r_q = (4 j + q) / n of the band and column c_q = (4 j + q) % n, the same in
+// every band: the per-column operands are loaded once, and the thread keeps
+// the column sums of its four elements (rows in ascending order), which go to
+// partial row y B + r_q of partials [S B x 3 x n] (k = 0 d_prenorm, 1 dNorm_w,
+// 2 dNorm_b; 1 and 2 only with a norm).  The backward adds all partial rows
+// for the bias / norm-parameter update, so it does not read the three
+// [rows x n] buffers again.  Workgroup (x, y) owns chunks [256 x, 256 (x + 1))
+// of the bands [y per, (y + 1) per); ERR_UB bands of every operand are loaded
+// before any is computed.
+constexpr int ERR_UB = 4;
+struct FlatPos {
+    uint32_t r[4], c[4];
+};
+struct ErrCol {   // per-column operands of the 4 elements
+    f32x4 nw, rstd;
+};
+
+template <typename T, bool FROM_SUM, int B, bool NORM, int UB>
+__device__ __forceinline__ void err_flat_bands(const ErrArgs &a, uint32_t b, uint32_t j, uint32_t s_ld,
+                                               const FlatPos &fp, const ErrCol &col, ErrAcc &acc) {
+    const uint32_t n = a.n;
+    f32x4 x[3][UB], mk[UB], pc[UB], rs[UB];
+#pragma unroll
+    for (int u = 0; u < UB; ++u) {
+        const uint32_t row0 = (b + u) * B;
+        const uint64_t base = (uint64_t)row0 * n + 4ull * j;
+        if constexpr (FROM_SUM) {
+            // (one 16-byte load when B == 1: the four addresses are consecutive)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                x[0][u][q] = a.s[(uint64_t)(row0 + fp.r[q]) * s_ld + fp.c[q]];
+            x[1][u] = load4<T>(a.predrop, base);
+            x[2][u] = load4<T>(a.preact, base);
+            mk[u] = load4<T>(a.mask, base);
+        } else {
+            x[0][u] = load4<T>(a.out, base);
+            x[1][u] = load4<T>(a.target, base);
+            x[2][u] = load4<T>(a.preact, base);
+        }
+        if constexpr (NORM) {
+            pc[u] = load4<T>(a.norm_in, base);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                rs[u][q] = (B == 1 && q > 0) ? rs[u][0] : to_f32(ldv<T>(a.norm_rstd, row0 + fp.r[q]));
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < UB; ++u) {
+        const uint64_t base = (uint64_t)(b + u) * B * n + 4ull * j;
+        f32x4 e;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            if constexpr (FROM_SUM)
+                e[q] = mk[u][q] * activation_derivative(a.act, x[0][u][q], x[1][u][q], x[2][u][q], a.leaky);
+            else
+                e[q] = output_err1(a, x[0][u][q], x[1][u][q], x[2][u][q]);
+        }
+        store4<float>(a.grad, base, e);
+        f32x4 dp = e * a.loss_scale;
+        if constexpr (NORM) {
+            f32x4 dnw, dnb;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                // BatchNorm's rstd is per column; the row value loaded for it is not used
+                const ErrOut o = err_norm1(a, e[q], pc[u][q], a.norm == 3 ? col.rstd[q] : rs[u][q], col.nw[q]);
+                dp[q] = o.dp;
+                dnw[q] = o.dnw;
+                dnb[q] = o.dnb;
+            }
+            store4<float>(a.d_norm_w, base, dnw);
+            store4<float>(a.d_norm_b, base, dnb);
+            acc.nw += dnw;
+            acc.nb += dnb;
+        }
+        store4<float>(a.d_prenorm, base, dp);
+        if (a.d_prenorm_h) store4<half_t>(a.d_prenorm_h, base, dp);
+        acc.dp += dp;
+    }
+}
+
+// The last band when rows % B != 0: element by element, rows past the end skipped.
+template <typename T, bool FROM_SUM, int B>
+__device__ __forceinline__ void err_flat_tail(const ErrArgs &a, uint32_t b, uint32_t s_ld, const FlatPos &fp,
+                                              const ErrCol &col, ErrAcc &acc) {
+    const uint32_t n = a.n;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t row = b * B + fp.r[q];
+        if (row >= a.rows) continue;
+        const uint64_t i = (uint64_t)row * n + fp.c[q];
+        float e;
+        if constexpr (FROM_SUM) {
+            const float sv = a.s[(uint64_t)row * s_ld + fp.c[q]];
+            e = to_f32(ldv<T>(a.mask, i)) *
+                activation_derivative(a.act, sv, to_f32(ldv<T>(a.predrop, i)), to_f32(ldv<T>(a.preact, i)), a.leaky);
+        } else {
+            e = output_err1(a, to_f32(ldv<T>(a.out, i)), to_f32(ldv<T>(a.target, i)), to_f32(ldv<T>(a.preact, i)));
+        }
+        const float pcv = a.norm ? to_f32(ldv<T>(a.norm_in, i)) : 0.0f;
+        const float rstd = (a.norm == 1 || a.norm == 2) ? to_f32(ldv<T>(a.norm_rstd, row)) : col.rstd[q];
+        const ErrOut o = err_norm1(a, e, pcv, rstd, col.nw[q]);
+        a.grad[i] = e;
+        if (a.norm) {
+            a.d_norm_w[i] = o.dnw;
+            a.d_norm_b[i] = o.dnb;
+        }
+        a.d_prenorm[i] = o.dp;
+        if (a.d_prenorm_h) a.d_prenorm_h[i] = (half_t)o.dp;
+        acc.dp[q] += o.dp;
+        acc.nw[q] += o.dnw;
+        acc.nb[q] += o.dnb;
+    }
+}
+
+template <typename T, bool FROM_SUM, int B, bool NORM>
+__global__ void __launch_bounds__(256) error_flat_kernel(ErrArgs a, float *__restrict__ partials, uint32_t per) {
+    const uint32_t n = a.n;
+    const uint32_t j = blockIdx.x * 256 + threadIdx.x;
+    if ((uint64_t)j * 4 >= (uint64_t)B * n) return;
+    FlatPos fp;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t e = 4 * j + q;
+        fp.r[q] = B == 1 ? 0u : e / n;
+        fp.c[q] = e - fp.r[q] * n;
+    }
+    ErrCol col{{0, 0, 0, 0}, {0, 0, 0, 0}};
+    if constexpr (NORM) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) col.nw[q] = a.nw[fp.c[q]];
+        if (a.norm == 3) {   // BatchNorm: rstd per column
+#pragma unroll
+            for (int q = 0; q < 4; ++q) col.rstd[q] = to_f32(ldv<T>(a.norm_rstd, fp.c[q]));
+        }
+    }
+    const uint32_t s_ld = a.s_ld ? a.s_ld : n;
+    const uint32_t full = a.rows / B, bands = (a.rows + B - 1) / B;
+    const uint32_t b0 = blockIdx.y * per, b1 = min(bands, b0 + per), bf = min(b1, full);
+    ErrAcc acc{{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
+    uint32_t b = b0;
+    for (; b + ERR_UB <= bf; b += ERR_UB) err_flat_bands<T, FROM_SUM, B, NORM, ERR_UB>(a, b, j, s_ld, fp, col, acc);
+    for (; b < bf; ++b) err_flat_bands<T, FROM_SUM, B, NORM, 1>(a, b, j, s_ld, fp, col, acc);
+    if (b < b1) err_flat_tail<T, FROM_SUM, B>(a, b, s_ld, fp, col, acc);
+    float *p = partials + (uint64_t)blockIdx.y * B * 3 * n;
+    if constexpr (B == 1) {
+        store4<float>(p, 4ull * j, acc.dp);
+        if constexpr (NORM) {
+            store4<float>(p + n, 4ull * j, acc.nw);
+            store4<float>(p + 2 * (uint64_t)n, 4ull * j, acc.nb);
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            float *pr = p + (uint64_t)fp.r[q] * 3 * n + fp.c[q];
+            pr[0] = acc.dp[q];
+            if constexpr (NORM) {
+                pr[n] = acc.nw[q];
+                pr[2 * (uint64_t)n] = acc.nb[q];
+            }
+        }
+    }
+}
+
+// Buffers at any alignment (a row-strided array or a per-column vector not
+// 16-byte aligned): a thread owns 4 consecutive columns of one row (cnt <= 4 of
+// them exist), read as the aligned 4-element chunk holding the group's first
+// element plus, when the group runs into the next chunk, that chunk too.  Each
+// chunk read holds an element of the group, so no read leaves the 16-byte
+// blocks the group's own elements lie in.  Stores split the group at the chunk
+// boundary into aligned 1-, 2- and 4-element pieces.  Only the lane that holds
+// a row's last, partial group (cnt < 4) takes the element-by-element path.
 template <typename T> struct GrpUA {
     __device__ __forceinline__ static uint32_t lead(const void *p) {
         return (uint32_t)((reinterpret_cast<uintptr_t>(p) / sizeof(T)) & 3u);
@@ -562,10 +738,10 @@ template <typename T> struct GrpUA {
         return pick(lo, hi, o);
     }
     __device__ __forceinline__ static f32x4 ld(const void *p, uint64_t i, uint32_t cnt) { return load<T>(p, i, cnt); }
-    __device__ __forceinline__ static f32x4 ldf(const float *p, uint64_t i, uint32_t cnt, bool = false) {
+    __device__ __forceinline__ static f32x4 ldf(const float *p, uint64_t i, uint32_t cnt) {
         return load<float>(p, i, cnt);
     }
-    __device__ __forceinline__ static void stf(float *p, uint64_t i, f32x4 v, uint32_t cnt, bool = false) {
+    __device__ __forceinline__ static void stf(float *p, uint64_t i, f32x4 v, uint32_t cnt) {
         if (cnt < 4) {
             for (uint32_t j = 0; j < cnt; ++j) p[i + j] = v[j];
             return;
@@ -621,191 +797,54 @@ template <typename T> struct GrpUA {
         }
     }
 };
-// GrpUA with the offset O of element i in its chunk known at compile time and
-// 4-element-aligned base pointers: no branches on the offset, and the picks
-// are register moves.
-template <typename T, int O> struct GrpUS {
-    template <typename E> __device__ __forceinline__ static f32x4 load(const void *p, uint64_t i, uint32_t cnt) {
-        const f32x4 lo = load4<E>(p, i - O);
-        if constexpr (O == 0) {
-            return lo;
-        } else {
-            const f32x4 hi = cnt > 4u - O ? load4<E>(p, i - O + 4) : f32x4{0, 0, 0, 0};
-            if constexpr (O == 1) return f32x4{lo[1], lo[2], lo[3], hi[0]};
-            if constexpr (O == 2) return f32x4{lo[2], lo[3], hi[0], hi[1]};
-            return f32x4{lo[3], hi[0], hi[1], hi[2]};
-        }
-    }
-    __device__ __forceinline__ static f32x4 ld(const void *p, uint64_t i, uint32_t cnt) { return load<T>(p, i, cnt); }
-    __device__ __forceinline__ static f32x4 ldf(const float *p, uint64_t i, uint32_t cnt, bool = false) {
-        return load<float>(p, i, cnt);
-    }
-    template <typename E, typename V2> __device__ __forceinline__ static void put(E *q, f32x4 v) {
-        // q = the group's first element; pieces at the chunk boundary
-        if constexpr (O == 0) {
-            if constexpr (sizeof(E) == 4)
-                *reinterpret_cast<f32x4 *>(q) = v;
-            else
-                *reinterpret_cast<f16x4 *>(q) = f16x4{(E)v[0], (E)v[1], (E)v[2], (E)v[3]};
-        } else if constexpr (O == 2) {
-            *reinterpret_cast<V2 *>(q) = V2{(E)v[0], (E)v[1]};
-            *reinterpret_cast<V2 *>(q + 2) = V2{(E)v[2], (E)v[3]};
-        } else {
-            q[0] = (E)v[0];
-            *reinterpret_cast<V2 *>(q + 1) = V2{(E)v[1], (E)v[2]};
-            q[3] = (E)v[3];
-        }
-    }
-    __device__ __forceinline__ static void stf(float *p, uint64_t i, f32x4 v, uint32_t cnt, bool = false) {
-        typedef float f32x2 __attribute__((ext_vector_type(2)));
-        if (cnt < 4) {
-            for (uint32_t j = 0; j < cnt; ++j) p[i + j] = v[j];
-            return;
-        }
-        put<float, f32x2>(p + i, v);
-    }
-    __device__ __forceinline__ static void sth(half_t *p, uint64_t i, f32x4 v, uint32_t cnt) {
-        typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-        if (cnt < 4) {
-            for (uint32_t j = 0; j < cnt; ++j) p[i + j] = (half_t)v[j];
-            return;
-        }
-        put<half_t, f16x2>(p + i, v);
-    }
-};
 
-// Accessor modes of the error kernels: 1 = GrpV (n % 4 == 0, aligned buffers);
-// 4 + n % 4 = GrpUS (aligned buffers, n % 4 != 0, row splits a multiple of 4
-// rows, so row rb + u with rb % 4 == 0 starts at offset (u n) % 4 of its
-// chunk); 0 = GrpUA (anything else).  RowAcc: the row-strided [rows x n]
-// arrays of row slot u; ColAcc: per-column vectors and the supplied sum s.
-template <typename T, int MODE, int U> struct RowAcc {
-    typedef typename std::conditional<
-        MODE == 1, GrpV<T>,
-        typename std::conditional<MODE == 0, GrpUA<T>, GrpUS<T, (U * (MODE - 4)) & 3>>::type>::type type;
-};
-template <typename T, int MODE> struct ColAcc {
-    typedef typename std::conditional<MODE == 0, GrpUA<T>, GrpV<T>>::type type;
-};
-
-// The three values of one 4-column group that feed the column sums of backward.cu:187-194.
-struct ErrSums4 {
-    f32x4 dp, dnw, dnb;
-};
-
-// grad = e; the element-local norm gradient (util.cu:175-215) into d_prenorm and
-// dNorm; d_prenorm scaled by the loss scale; its fp16 copy for the GEMMs.
-template <typename T, class G, class GC>
-__device__ __forceinline__ ErrSums4 write_err4(const ErrArgs &a, uint64_t idx, uint32_t row, uint32_t col,
-                                               uint32_t cnt, f32x4 e) {
-    G::stf(a.grad, idx, e, cnt, true);
-    ErrSums4 o;
-    o.dp = e;
-    o.dnw = o.dnb = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    if (a.norm) {
-        const f32x4 pv = a.norm == 1 ? G::ld(a.prenorm, idx, cnt) : f32x4{0, 0, 0, 0};
-        const f32x4 cv = a.norm >= 2 ? G::ld(a.centered, idx, cnt) : f32x4{0, 0, 0, 0};
-        const f32x4 nw = GC::ldf(a.nw, col, cnt);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float rstd = to_f32(ldv<T>(a.norm_rstd, a.norm == 3 ? col + (j < (int)cnt ? j : 0) : row));
-            const NormGrad g = norm_grad(a.norm, e[j], pv[j], cv[j], rstd, nw[j], a.inv_n, a.inv_m);
-            o.dp[j] = g.d_prenorm;
-            o.dnw[j] = g.dnw;
-            o.dnb[j] = g.dnb;
-        }
-        G::stf(a.d_norm_w, idx, o.dnw, cnt);
-        G::stf(a.d_norm_b, idx, o.dnb, cnt);
-    }
-    o.dp = o.dp * a.loss_scale;
-    G::stf(a.d_prenorm, idx, o.dp, cnt, true);
-    if (a.d_prenorm_h) G::sth(a.d_prenorm_h, idx, o.dp, cnt);
-    if (cnt < 4) {
-        // columns past n add nothing to the sums
-#pragma unroll
-        for (uint32_t j = 0; j < 4; ++j)
-            if (j >= cnt) o.dp[j] = o.dnw[j] = o.dnb[j] = 0.0f;
-    }
-    return o;
-}
-
-// Loss delta of one 4-column group (backward.cu:24-45).
-template <typename T, class G>
-__device__ __forceinline__ f32x4 output_err4(const ErrArgs &a, uint64_t idx, uint32_t cnt) {
-    const f32x4 out = G::ld(a.out, idx, cnt), tg = G::ld(a.target, idx, cnt), pre = G::ld(a.preact, idx, cnt);
-    f32x4 e;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const float o = activation(a.act, out[j], a.leaky);
-        float ej = 0.0f;
-        if (a.loss == 0) {
-            ej = activation_derivative(a.act, o - tg[j], o, pre[j], a.leaky);
-        } else if ((a.loss == 1 && a.act == 5) || (a.loss == 2 && a.act == 1)) {
-            ej = o - tg[j];
-        }
-        e[j] = ej;
-    }
-    return e;
-}
-
-// Error + column sums in one pass (backward.cu:12-56 for the output layer,
-// 79-100 for a supplied sum s).  Workgroup (x, y) owns the columns
-// [1024 x, 1024 (x + 1)) of the rows [y per, (y + 1) per): a thread owns one
-// 4-column group, loads ERR_UR rows of its operands before computing any
-// (ERR_UR x 40 bytes in flight), writes grad / d_prenorm (/ dNorm) and adds
-// d_prenorm, dNorm_w and dNorm_b into running column sums, rows in ascending
-// order.  The sums go to partials[y][k][n] (k = 0 d_prenorm, 1 dNorm_w,
-// 2 dNorm_b; 1 and 2 only with a norm), the inputs of the bias / norm-
-// parameter update, so the backward does not read the three [rows x n]
-// buffers again.  4 rows per thread and ~1024 workgroups: of the shapes
-// measured on the C3 step (rows x column groups per thread in {4x1, 2x2, 1x4,
-// 2x4}, 512 to 2048 workgroups) the fastest, both alone and between the GEMMs.
+// The error kernel on GrpUA accesses: workgroup (x, y) owns the columns
+// [1024 x, 1024 (x + 1)) of the rows [y per, (y + 1) per), a thread one
+// 4-column group, ERR_UR rows loaded before any is computed (from a sum) or
+// row by row (output layer); column sums to partials[y][k][n].
 constexpr int ERR_UR = 4;
-struct ErrAcc {   // running column sums of one 4-column group
-    f32x4 dp, nw, nb;
-};
-template <typename T, bool FROM_SUM, int MODE, int U>
-__device__ __forceinline__ void err_load(const ErrArgs &a, uint32_t rb, uint32_t r1, uint32_t c, uint32_t cnt,
-                                         uint32_t s_ld, f32x4 (&x)[4][ERR_UR]) {
-    typedef typename RowAcc<T, MODE, U>::type G;
-    typedef typename ColAcc<float, MODE>::type GS;
-    if (rb + U >= r1) return;
-    const uint64_t idx = (uint64_t)(rb + U) * a.n + c;
-    x[0][U] = GS::ldf(a.s, (uint64_t)(rb + U) * s_ld + c, cnt, true);
-    x[1][U] = G::ld(a.predrop, idx, cnt);
-    x[2][U] = G::ld(a.preact, idx, cnt);
-    x[3][U] = G::ld(a.mask, idx, cnt);
-}
-template <typename T, bool FROM_SUM, int MODE, int U>
-__device__ __forceinline__ void err_row(const ErrArgs &a, uint32_t rb, uint32_t r1, uint32_t c, uint32_t cnt,
-                                        const f32x4 (&x)[4][ERR_UR], ErrAcc &acc) {
-    typedef typename RowAcc<T, MODE, U>::type G;
-    typedef typename ColAcc<float, MODE>::type GC;
-    const uint32_t row = rb + U;
-    if (row >= r1) return;
+template <typename T, bool FROM_SUM>
+__device__ __forceinline__ void err_row_ua(const ErrArgs &a, uint32_t row, uint32_t c, uint32_t cnt, f32x4 s,
+                                           f32x4 pd, f32x4 pa, f32x4 mk, ErrAcc &acc) {
+    typedef GrpUA<T> G;
     const uint64_t idx = (uint64_t)row * a.n + c;
     f32x4 e;
     if constexpr (FROM_SUM) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            e[j] = x[3][U][j] * activation_derivative(a.act, x[0][U][j], x[1][U][j], x[2][U][j], a.leaky);
+        for (int j = 0; j < 4; ++j) e[j] = mk[j] * activation_derivative(a.act, s[j], pd[j], pa[j], a.leaky);
     } else {
-        e = output_err4<T, G>(a, idx, cnt);
+        const f32x4 out = G::ld(a.out, idx, cnt), tg = G::ld(a.target, idx, cnt), pre = G::ld(a.preact, idx, cnt);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) e[j] = output_err1(a, out[j], tg[j], pre[j]);
     }
-    const ErrSums4 o = write_err4<T, G, GC>(a, idx, row, c, cnt, e);
-    acc.dp += o.dp;
-    acc.nw += o.dnw;
-    acc.nb += o.dnb;
+    G::stf(a.grad, idx, e, cnt);
+    f32x4 dp, dnw, dnb;
+    const f32x4 pc = a.norm ? G::ld(a.norm_in, idx, cnt) : f32x4{0, 0, 0, 0};
+    const f32x4 nw = a.norm ? GrpUA<float>::ldf(a.nw, c, cnt) : f32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float rstd =
+            a.norm ? to_f32(ldv<T>(a.norm_rstd, a.norm == 3 ? c + (j < (int)cnt ? j : 0) : row)) : 0.0f;
+        const ErrOut o = err_norm1(a, e[j], pc[j], rstd, nw[j]);
+        const bool live = j < (int)cnt;   // columns past n add nothing to the sums
+        dp[j] = live ? o.dp : 0.0f;
+        dnw[j] = live ? o.dnw : 0.0f;
+        dnb[j] = live ? o.dnb : 0.0f;
+    }
+    if (a.norm) {
+        G::stf(a.d_norm_w, idx, dnw, cnt);
+        G::stf(a.d_norm_b, idx, dnb, cnt);
+    }
+    G::stf(a.d_prenorm, idx, dp, cnt);
+    if (a.d_prenorm_h) G::sth(a.d_prenorm_h, idx, dp, cnt);
+    acc.dp += dp;
+    acc.nw += dnw;
+    acc.nb += dnb;
 }
-template <typename T, bool FROM_SUM, int MODE, int... U>
-__device__ __forceinline__ void err_rows(const ErrArgs &a, uint32_t rb, uint32_t r1, uint32_t c, uint32_t cnt,
-                                         uint32_t s_ld, ErrAcc &acc, std::integer_sequence<int, U...>) {
-    f32x4 x[4][ERR_UR];
-    if constexpr (FROM_SUM) (err_load<T, FROM_SUM, MODE, U>(a, rb, r1, c, cnt, s_ld, x), ...);
-    (err_row<T, FROM_SUM, MODE, U>(a, rb, r1, c, cnt, x, acc), ...);
-}
-template <typename T, bool FROM_SUM, int MODE>
+
+template <typename T, bool FROM_SUM>
 __global__ void __launch_bounds__(256) error_cols_kernel(ErrArgs a, float *__restrict__ partials, uint32_t per) {
+    typedef GrpUA<T> G;
     const uint32_t c = blockIdx.x * 1024 + threadIdx.x * 4;
     if (c >= a.n) return;
     const uint32_t cnt = min(4u, a.n - c);
@@ -813,23 +852,35 @@ __global__ void __launch_bounds__(256) error_cols_kernel(ErrArgs a, float *__res
     const uint32_t r0 = blockIdx.y * per;
     const uint32_t r1 = min(a.rows, r0 + per);
     ErrAcc acc{{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
-    for (uint32_t rb = r0; rb < r1; rb += ERR_UR)
-        err_rows<T, FROM_SUM, MODE>(a, rb, r1, c, cnt, s_ld, acc, std::make_integer_sequence<int, ERR_UR>{});
-    typedef typename std::conditional<MODE == 1, GrpV<float>, GrpUA<float>>::type GP;
+    for (uint32_t rb = r0; rb < r1; rb += ERR_UR) {
+        f32x4 s[ERR_UR] = {}, pd[ERR_UR] = {}, pa[ERR_UR] = {}, mk[ERR_UR] = {};
+#pragma unroll
+        for (int u = 0; u < ERR_UR; ++u) {
+            if (!FROM_SUM || rb + u >= r1) continue;
+            const uint64_t idx = (uint64_t)(rb + u) * a.n + c;
+            s[u] = GrpUA<float>::ldf(a.s, (uint64_t)(rb + u) * s_ld + c, cnt);
+            pd[u] = G::ld(a.predrop, idx, cnt);
+            pa[u] = G::ld(a.preact, idx, cnt);
+            mk[u] = G::ld(a.mask, idx, cnt);
+        }
+#pragma unroll
+        for (int u = 0; u < ERR_UR; ++u)
+            if (rb + u < r1) err_row_ua<T, FROM_SUM>(a, rb + u, c, cnt, s[u], pd[u], pa[u], mk[u], acc);
+    }
     float *p = partials + (uint64_t)blockIdx.y * 3 * a.n + c;
-    GP::stf(p, 0, acc.dp, cnt);
+    GrpUA<float>::stf(p, 0, acc.dp, cnt);
     if (a.norm) {
-        GP::stf(p + a.n, 0, acc.nw, cnt);
-        GP::stf(p + 2 * a.n, 0, acc.nb, cnt);
+        GrpUA<float>::stf(p + a.n, 0, acc.nw, cnt);
+        GrpUA<float>::stf(p + 2 * a.n, 0, acc.nb, cnt);
     }
 }
 
 static bool a16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Every buffer the kernel touches 16-byte aligned, and s's rows a multiple of 4
-// elements apart (partials only matter for GrpV: GrpUS writes them via GrpUA).
+// Every buffer the flat kernel touches 16-byte aligned (s at any row pitch: a
+// pitch other than n is read element by element); partials only when n % 4 == 0
+// (its 4-element stores).
 static bool err_aligned(const ErrArgs &a, bool from_sum, const float *partials) {
-    if (from_sum && (a.s_ld & 3u) != 0) return false;
     const void *ptrs[] = {a.grad, a.d_prenorm, a.d_prenorm_h, a.preact, a.norm ? a.nw : nullptr,
                           a.norm ? a.d_norm_w : nullptr, a.norm ? a.d_norm_b : nullptr,
                           a.norm == 1 ? a.prenorm : nullptr, a.norm >= 2 ? a.centered : nullptr,
@@ -840,54 +891,65 @@ static bool err_aligned(const ErrArgs &a, bool from_sum, const float *partials) 
     return true;
 }
 
-// Row splits of the error kernels: ~1024 workgroups of >= 16 rows for n >= 1024;
-// narrower outputs leave most of a workgroup's 256 column-group lanes idle, so
-// they get ~256K active lanes in all, in slices of >= 4 rows (at most 4096).
+// Rows per band of the flat error kernel: 4 / gcd(n, 4).
+static uint32_t err_band(uint32_t n) { return (n & 3u) == 0 ? 1u : (n & 1u) ? 4u : 2u; }
+
+// Partial-sum rows of the error kernels: S row slices x err_band(n).  ~1024
+// workgroups of >= 16 rows when a band has >= 256 chunks; narrower outputs
+// leave most of a workgroup's lanes idle, so they get ~256K active lanes in
+// all, in slices of >= 4 rows (at most 4096 slices).
 uint32_t err_col_splits(uint32_t rows, uint32_t n) {
+    const uint32_t band = err_band(n);
+    const uint64_t chunks = (uint64_t)band * n / 4;   // lanes per band
     uint32_t sp, cap;
-    if (n >= 1024) {
-        sp = cdiv(1024, cdiv(n, 1024));
+    if (chunks >= 256) {
+        sp = cdiv(1024, cdiv(chunks, 256));
         cap = cdiv(rows, 16);
     } else {
-        sp = cdiv(262144u, cdiv(n, 4));
+        sp = cdiv(262144u, chunks ? chunks : 1);
         cap = cdiv(rows, 4);
     }
     if (sp > cap) sp = cap;
+    if (sp > cdiv(rows, band)) sp = cdiv(rows, band);
     if (sp > 4096) sp = 4096;
-    return sp < 1 ? 1 : sp;
+    return (sp < 1 ? 1 : sp) * band;
 }
 
-template <bool FROM_SUM, typename T, int MODE>
-static void launch_error_mode(const ErrArgs &a, float *partials, uint32_t splits, uint32_t per, hipStream_t s) {
-    hipLaunchKernelGGL((error_cols_kernel<T, FROM_SUM, MODE>), dim3(cdiv(a.n, 1024), splits), dim3(256), 0, s, a,
-                       partials, per);
+template <bool FROM_SUM, typename T, int B>
+static void launch_error_flat(const ErrArgs &a, float *partials, uint32_t splits, hipStream_t s) {
+    const uint32_t S = splits / B;
+    const uint32_t per = cdiv(cdiv(a.rows, B), S);
+    const dim3 grid(cdiv((uint64_t)B * a.n, 1024), S);
+    if (a.norm)
+        hipLaunchKernelGGL((error_flat_kernel<T, FROM_SUM, B, true>), grid, dim3(256), 0, s, a, partials, per);
+    else
+        hipLaunchKernelGGL((error_flat_kernel<T, FROM_SUM, B, false>), grid, dim3(256), 0, s, a, partials, per);
 }
 
+// splits: the partial-sum rows, from err_col_splits.
 template <bool FROM_SUM, typename T>
-static void launch_error_t(const ErrArgs &a, float *partials, uint32_t splits, hipStream_t s) {
-    const uint32_t per = cdiv(a.rows, splits);
+static hipError_t launch_error_t(const ErrArgs &a0, float *partials, uint32_t splits, hipStream_t s) {
+    ErrArgs a = a0;
+    a.norm_in = a.norm == 1 ? a.prenorm : a.centered;
     if (!err_aligned(a, FROM_SUM, partials)) {
-        launch_error_mode<FROM_SUM, T, 0>(a, partials, splits, per, s);
-        return;
+        hipLaunchKernelGGL((error_cols_kernel<T, FROM_SUM>), dim3(cdiv(a.n, 1024), splits), dim3(256), 0, s, a,
+                           partials, cdiv(a.rows, splits));
+        return hipGetLastError();
     }
-    // GrpUS needs every row slice to start on a multiple of 4 rows; the last
-    // slices may then be empty (their partial sums are zeros)
-    const uint32_t per4 = (per + 3u) & ~3u;
-    switch (a.n & 3u) {
-    case 0: launch_error_mode<FROM_SUM, T, 1>(a, partials, splits, per, s); break;
-    case 1: launch_error_mode<FROM_SUM, T, 5>(a, partials, splits, per4, s); break;
-    case 2: launch_error_mode<FROM_SUM, T, 6>(a, partials, splits, per4, s); break;
-    default: launch_error_mode<FROM_SUM, T, 7>(a, partials, splits, per4, s); break;
+    const uint32_t band = err_band(a.n);
+    if (splits < band || splits % band) return hipErrorInvalidValue;
+    switch (band) {
+    case 1: launch_error_flat<FROM_SUM, T, 1>(a, partials, splits, s); break;
+    case 2: launch_error_flat<FROM_SUM, T, 2>(a, partials, splits, s); break;
+    default: launch_error_flat<FROM_SUM, T, 4>(a, partials, splits, s); break;
     }
+    return hipGetLastError();
 }
 
 hipError_t launch_output_error(const ErrArgs &a, float *partials, uint32_t splits, hipStream_t s) {
     if ((uint64_t)a.rows * a.n == 0) return hipSuccess;
-    if (a.dtype == 1)
-        launch_error_t<false, half_t>(a, partials, splits, s);
-    else
-        launch_error_t<false, float>(a, partials, splits, s);
-    return hipGetLastError();
+    return a.dtype == 1 ? launch_error_t<false, half_t>(a, partials, splits, s)
+                        : launch_error_t<false, float>(a, partials, splits, s);
 }
 
 hipError_t launch_error_from_sum(const ErrArgs &a0, float *partials, uint32_t splits, hipStream_t s) {
@@ -900,11 +962,8 @@ hipError_t launch_error_from_sum(const ErrArgs &a0, float *partials, uint32_t sp
     ErrArgs a = a0;
     if (!act_uses_output(a.act)) a.predrop = a.mask;
     if (!act_uses_input(a.act)) a.preact = a.mask;
-    if (a.dtype == 1)
-        launch_error_t<true, half_t>(a, partials, splits, s);
-    else
-        launch_error_t<true, float>(a, partials, splits, s);
-    return hipGetLastError();
+    return a.dtype == 1 ? launch_error_t<true, half_t>(a, partials, splits, s)
+                        : launch_error_t<true, float>(a, partials, splits, s);
 }
 
 // ---- column sums (backward.cu:187-194) + vector optimiser (backward.cu:198-225) -------

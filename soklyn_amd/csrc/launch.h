@@ -129,15 +129,17 @@ struct ErrArgs {
     uint32_t s_ld, pad;                                // row pitch of s (0 = n)
     const void *predrop, *mask;                        // error_from_sum
     const void *norm_rstd, *centered, *prenorm;
+    const void *norm_in;                               // set by the launchers: prenorm (RMS) or centered
     const float *nw;
     float *grad, *d_prenorm, *d_norm_w, *d_norm_b;
     half_t *d_prenorm_h;
 };
-// Both also write the column sums of d_prenorm / dNorm_w / dNorm_b over the
-// rows into partials [splits x 3 x n] (splits from err_col_splits).
+// Both also write partial column sums of d_prenorm / dNorm_w / dNorm_b into
+// partials [splits x 3 x n]; their sum over the splits rows is the column sum
+// over all rows.  splits must come from err_col_splits.
 hipError_t launch_output_error(const ErrArgs &a, float *partials, uint32_t splits, hipStream_t s);
 hipError_t launch_error_from_sum(const ErrArgs &a, float *partials, uint32_t splits, hipStream_t s);
-// Row splits the error kernels use for their column sums.
+// Partial-sum rows the error kernels write for [rows x n].
 uint32_t err_col_splits(uint32_t rows, uint32_t n);
 
 // Column sums of up to three fp32 [rows x n] arrays into partials

@@ -1,9 +1,13 @@
-"""Parity of the error and norm kernels on rows that do not start on a 4-element boundary:
-an odd output width (every row at a different offset) and buffers whose base
-pointers sit 1..3 elements past a 16-byte boundary (torch views into a larger
-allocation).  These take the 4-column-group path that reads aligned chunks and
-splits its stores at chunk boundaries; the column sums it leaves feed the
-backward's bias and norm-parameter update, checked through the moments.
+"""Parity of the error and norm kernels on rows that do not start on a 4-element boundary.
+
+Output widths with n % 4 != 0 on aligned buffers take the flat error kernel: a
+band of 4 / gcd(n, 4) rows is a whole number of aligned 4-element chunks, and
+widths under 4 put one chunk across several rows; batches that are not a
+multiple of the band end in a partial band done element by element.  Buffers
+whose base pointers sit 1..3 elements past a 16-byte boundary (torch views into
+a larger allocation) take the 4-column-group path that reads aligned chunks and
+splits its stores at chunk boundaries.  The column sums either path leaves feed
+the backward's bias and norm-parameter update, checked through the moments.
 
 Gates as everywhere: fp32 1e-4 normwise and 1e-2 elementwise, fp16 2e-2 normwise against the oracle.
 """
@@ -73,6 +77,7 @@ def _run(ctx, half, M, K, N, norm, act, off):
     (300, 64, 1022, 1, abi.ACT_MISH),    # RMSNorm, width 2 mod 4
     (257, 48, 13, 0, abi.ACT_SILU),      # width < 4 columns per group tail
     (64, 32, 1027, 3, abi.ACT_TANH),     # batch norm (per-column statistics)
+    (299, 40, 70, 2, abi.ACT_SIGMOID),   # width 2 mod 4 with a last band of one row
 ])
 def test_error_odd_width(ctx, half, M, K, N, norm, act):
     _run(ctx, half, M, K, N, norm, act, 0)
@@ -85,9 +90,11 @@ def test_error_misaligned_buffers(ctx, half, off):
 
 
 @pytest.mark.parametrize("half", [True, False])
-def test_output_error_odd_width(ctx, half):
-    M, K, N = 515, 40, 13
-    ob, db = make_pair(ctx, K, N, M, seed=71, half=half, norm=2)
+@pytest.mark.parametrize("M,N,norm", [(515, 13, 2), (203, 1, 0), (130, 2, 0), (77, 3, 1)])
+def test_output_error_odd_width(ctx, half, M, N, norm):
+    """Widths under 4 put one 4-element chunk across several rows."""
+    K = 40
+    ob, db = make_pair(ctx, K, N, M, seed=71 + N, half=half, norm=norm)
     x = inputs(72, M, K, half)
     ob.forward(x, M)
     db.forward(dev(x, half), M)
@@ -97,7 +104,7 @@ def test_output_error_odd_width(ctx, half):
     db.output_error(dev(t, half), abi.LOSS_BCE, abi.ACT_SIGMOID)
     torch.cuda.synchronize()
     tol = FP16_TOL if half else FP32_TOL
-    for n in ("grad", "d_prenorm", "d_norm_w", "d_norm_b"):
+    for n in ("grad", "d_prenorm") + (("d_norm_w", "d_norm_b") if norm else ()):
         check(n, db.get(n), getattr(ob, n), tol)
 
 

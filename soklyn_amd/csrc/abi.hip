@@ -768,6 +768,53 @@ static int32_t hidden_error_impl(skl_ctx *ctx, const skl_dense_desc *cur, const 
     if ((r = zero_dnorm_tail(ctx, cur, batch))) return r;
     ctx->cs.valid = false;
 
+    // act' * mask and the element-local norm gradient (backward.cu:79-100), with the
+    // column sums of d_prenorm / dNorm for cur's backward
+    ErrArgs a{};
+    a.dtype = cur->dtype;
+    a.rows = batch;
+    a.n = cur->outputs;
+    a.norm = cur->norm;
+    a.act = cur->act;
+    a.leaky = cur->act == SKL_ACT_LEAKY_RELU ? cur->leaky : 0.0f;
+    a.inv_n = 1.0f / (float)cur->outputs;
+    a.inv_m = 1.0f / (float)batch;
+    a.loss_scale = 1.0f;
+    a.predrop = cur->predrop;
+    a.preact = cur->preact;
+    a.mask = cur->mask;
+    a.norm_rstd = cur->norm_rstd;
+    a.centered = cur->centered;
+    a.prenorm = cur->prenorm;
+    a.nw = master_norm_w(cur);
+    a.grad = cur->grad;
+    a.d_prenorm = cur->d_prenorm;
+    a.d_norm_w = cur->d_norm_w;
+    a.d_norm_b = cur->d_norm_b;
+    a.d_prenorm_h = cur->dtype == SKL_F16 ? reinterpret_cast<half_t *>(cur->d_prenorm_h) : nullptr;
+    const void *next_dp = cur->dtype == SKL_F16 ? next->d_prenorm_h : next->d_prenorm;
+
+    // A next layer of at most 16 outputs: its GEMM would pad k to 128, so the
+    // error kernel forms s = next.d_prenorm . next.W^T itself, per element, from
+    // fp32 copies of the two operands padded to 16 columns (same operands as the
+    // GEMM: f16(d_prenorm) and the working W for fp16 blocks).
+    if (next->outputs <= 16) {
+        uint32_t splits = 0;
+        if ((r = ensure_cols(ctx, batch, cur->outputs, &splits))) return r;
+        const size_t a_bytes = ((size_t)batch * 16 * sizeof(float) + 255) & ~(size_t)255;
+        if ((r = ensure_ws(ctx, a_bytes + (size_t)cur->outputs * 16 * sizeof(float)))) return r;
+        a.sk_a = reinterpret_cast<const float *>(ctx->ws);
+        a.sk_w = reinterpret_cast<const float *>(reinterpret_cast<char *>(ctx->ws) + a_bytes);
+        if (err_skinny_ok(a, ctx->cols)) {
+            SKL_TRY(launch_skinny_operands(cur->dtype, next_dp, batch, next->w, cur->outputs, next->outputs,
+                                           const_cast<float *>(a.sk_a), const_cast<float *>(a.sk_w), ctx->stream));
+            SKL_TRY(launch_error_skinny(a, ctx->cols, splits, ctx->stream));
+            record_cols(ctx, cur, batch, splits);
+            return SKL_OK;
+        }
+        a.sk_a = a.sk_w = nullptr;
+    }
+
     // s = next.d_prenorm . next.W^T into the workspace (backward.cu:72-77; fp16:
     // f16(d_prenorm) and the working W, == f16(master) after every update) ...
     GemmLaunch g{};
@@ -779,7 +826,7 @@ static int32_t hidden_error_impl(skl_ctx *ctx, const skl_dense_desc *cur, const 
     g.ldb = next->outputs;
     g.a_kcontig = true;
     g.b_kcontig = true;
-    g.A = cur->dtype == SKL_F16 ? next->d_prenorm_h : next->d_prenorm;
+    g.A = next_dp;
     g.B = next->w;
     g.splits = 1;
     g.op = Op::InputGrad;
@@ -827,32 +874,9 @@ static int32_t hidden_error_impl(skl_ctx *ctx, const skl_dense_desc *cur, const 
     g.st.ldc = s_ld;
     if ((r = exec_gemm(ctx, g, plan, reinterpret_cast<char *>(ctx->ws) + s_bytes, true))) return r;
 
-    // ... then act' * mask and the element-local norm gradient (backward.cu:79-100), with
-    // the column sums of d_prenorm / dNorm for cur's backward
-    ErrArgs a{};
-    a.dtype = cur->dtype;
-    a.rows = batch;
-    a.n = cur->outputs;
-    a.norm = cur->norm;
-    a.act = cur->act;
-    a.leaky = cur->act == SKL_ACT_LEAKY_RELU ? cur->leaky : 0.0f;
-    a.inv_n = 1.0f / (float)cur->outputs;
-    a.inv_m = 1.0f / (float)batch;
-    a.loss_scale = 1.0f;
+    // ... then the error kernel on it
     a.s = sum;
     a.s_ld = s_ld;
-    a.predrop = cur->predrop;
-    a.preact = cur->preact;
-    a.mask = cur->mask;
-    a.norm_rstd = cur->norm_rstd;
-    a.centered = cur->centered;
-    a.prenorm = cur->prenorm;
-    a.nw = master_norm_w(cur);
-    a.grad = cur->grad;
-    a.d_prenorm = cur->d_prenorm;
-    a.d_norm_w = cur->d_norm_w;
-    a.d_norm_b = cur->d_norm_b;
-    a.d_prenorm_h = cur->dtype == SKL_F16 ? reinterpret_cast<half_t *>(cur->d_prenorm_h) : nullptr;
     uint32_t splits = 0;
     if ((r = ensure_cols(ctx, batch, cur->outputs, &splits))) return r;
     SKL_TRY(launch_error_from_sum(a, ctx->cols, splits, ctx->stream));

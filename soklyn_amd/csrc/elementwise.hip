@@ -538,42 +538,67 @@ struct ErrAcc {   // running column sums of a thread's 4 elements
 };
 
 // Error + column sums in one pass (backward.cu:12-56 for the output layer,
-// 79-100 for a supplied sum s), on 16-byte aligned buffers: the [rows x n]
-// arrays as one flat array.  A band of B = 4 / gcd(n, 4) rows holds B n / 4
-// whole 4-element chunks; thread j owns chunk j of every band of its row
-// slice, so each load and store of a row-strided array is one 16-byte (fp32)
-// or 8-byte (fp16) access whatever n is.  Element q of the chunk lies in row
-// r_q = (4 j + q) / n of the band and column c_q = (4 j + q) % n, the same in
-// every band: the per-column operands are loaded once, and the thread keeps
-// the column sums of its four elements (rows in ascending order), which go to
-// partial row y B + r_q of partials [S B x 3 x n] (k = 0 d_prenorm, 1 dNorm_w,
-// 2 dNorm_b; 1 and 2 only with a norm).  The backward adds all partial rows
-// for the bias / norm-parameter update, so it does not read the three
-// [rows x n] buffers again.  Workgroup (x, y) owns chunks [256 x, 256 (x + 1))
-// of the bands [y per, (y + 1) per); ERR_UB bands of every operand are loaded
-// before any is computed.
+// 79-100 for the hidden error from the sum s), on 16-byte aligned buffers: the
+// [rows x n] arrays as one flat array.  A band of B = 4 / gcd(n, 4) rows holds
+// B n / 4 whole 4-element chunks; thread j owns chunk j of every band of its
+// row slice, so each load and store of a row-strided array is one 16-byte
+// (fp32) or 8-byte (fp16) access whatever n is.  Element q of the chunk lies
+// in row r_q = (4 j + q) / n of the band and column c_q = (4 j + q) % n, the
+// same in every band: the per-column operands are loaded once, and the thread
+// keeps the column sums of its four elements (rows in ascending order), which
+// go to partial row y B + r_q of partials [S B x 3 x n] (k = 0 d_prenorm,
+// 1 dNorm_w, 2 dNorm_b; 1 and 2 only with a norm).  The backward adds all
+// partial rows for the bias / norm-parameter update, so it does not read the
+// three [rows x n] buffers again.  Workgroup (x, y) owns chunks
+// [256 x, 256 (x + 1)) of the bands [y per, (y + 1) per); UB bands of every
+// operand are loaded before any is computed.
+//
+// SRC: 0 the output layer's loss delta, 1 the hidden error from s in memory,
+// 2 the hidden error with s = A . W^T formed per element (backward.cu:72-77
+// for a next layer of at most 16 outputs: A [rows x 16] and W [n x 16] are
+// fp32 zero-padded copies of the next layer's d_prenorm and weights, so an
+// element's sum is 16 FMAs over k in ascending order, and s never goes
+// through HBM).  With SRC 2 the thread keeps its four columns of W in
+// registers; the n >= 4 it needs puts a chunk's elements in at most two rows.
 constexpr int ERR_UB = 4;
 struct FlatPos {
     uint32_t r[4], c[4];
 };
 struct ErrCol {   // per-column operands of the 4 elements
     f32x4 nw, rstd;
+    f32x4 w[4][4];   // SRC 2: W's 16 values of each element's column
 };
 
-template <typename T, bool FROM_SUM, int B, bool NORM, int UB>
+template <int B> struct SkRows {   // SRC 2: A's rows of a chunk's first and last element
+    f32x4 lo[4], hi[B > 1 ? 4 : 1];
+};
+
+template <typename T, int SRC, int B, bool NORM, int UB>
 __device__ __forceinline__ void err_flat_bands(const ErrArgs &a, uint32_t b, uint32_t j, uint32_t s_ld,
                                                const FlatPos &fp, const ErrCol &col, ErrAcc &acc) {
     const uint32_t n = a.n;
     f32x4 x[3][UB], mk[UB], pc[UB], rs[UB];
+    SkRows<B> ar[SRC == 2 ? UB : 1];
 #pragma unroll
     for (int u = 0; u < UB; ++u) {
         const uint32_t row0 = (b + u) * B;
         const uint64_t base = (uint64_t)row0 * n + 4ull * j;
-        if constexpr (FROM_SUM) {
+        if constexpr (SRC == 1) {
             // (one 16-byte load when B == 1: the four addresses are consecutive)
 #pragma unroll
             for (int q = 0; q < 4; ++q)
                 x[0][u][q] = a.s[(uint64_t)(row0 + fp.r[q]) * s_ld + fp.c[q]];
+        } else if constexpr (SRC == 2) {
+            const f32x4 *lo = reinterpret_cast<const f32x4 *>(a.sk_a + (uint64_t)(row0 + fp.r[0]) * 16);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) ar[u].lo[i] = lo[i];
+            if constexpr (B > 1) {
+                const f32x4 *hi = reinterpret_cast<const f32x4 *>(a.sk_a + (uint64_t)(row0 + fp.r[3]) * 16);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) ar[u].hi[i] = hi[i];
+            }
+        }
+        if constexpr (SRC != 0) {
             x[1][u] = load4<T>(a.predrop, base);
             x[2][u] = load4<T>(a.preact, base);
             mk[u] = load4<T>(a.mask, base);
@@ -592,10 +617,23 @@ __device__ __forceinline__ void err_flat_bands(const ErrArgs &a, uint32_t b, uin
 #pragma unroll
     for (int u = 0; u < UB; ++u) {
         const uint64_t base = (uint64_t)(b + u) * B * n + 4ull * j;
+        if constexpr (SRC == 2) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const bool lo = B == 1 || fp.r[q] == fp.r[0];
+                float sv = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 16; ++k) {
+                    const float av = lo ? ar[u].lo[k / 4][k % 4] : ar[u].hi[B > 1 ? k / 4 : 0][k % 4];
+                    sv = __builtin_fmaf(av, col.w[q][k / 4][k % 4], sv);
+                }
+                x[0][u][q] = sv;
+            }
+        }
         f32x4 e;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            if constexpr (FROM_SUM)
+            if constexpr (SRC != 0)
                 e[q] = mk[u][q] * activation_derivative(a.act, x[0][u][q], x[1][u][q], x[2][u][q], a.leaky);
             else
                 e[q] = output_err1(a, x[0][u][q], x[1][u][q], x[2][u][q]);
@@ -624,7 +662,7 @@ __device__ __forceinline__ void err_flat_bands(const ErrArgs &a, uint32_t b, uin
 }
 
 // The last band when rows % B != 0: element by element, rows past the end skipped.
-template <typename T, bool FROM_SUM, int B>
+template <typename T, int SRC, int B>
 __device__ __forceinline__ void err_flat_tail(const ErrArgs &a, uint32_t b, uint32_t s_ld, const FlatPos &fp,
                                               const ErrCol &col, ErrAcc &acc) {
     const uint32_t n = a.n;
@@ -634,8 +672,15 @@ __device__ __forceinline__ void err_flat_tail(const ErrArgs &a, uint32_t b, uint
         if (row >= a.rows) continue;
         const uint64_t i = (uint64_t)row * n + fp.c[q];
         float e;
-        if constexpr (FROM_SUM) {
-            const float sv = a.s[(uint64_t)row * s_ld + fp.c[q]];
+        if constexpr (SRC != 0) {
+            float sv;
+            if constexpr (SRC == 1) {
+                sv = a.s[(uint64_t)row * s_ld + fp.c[q]];
+            } else {
+                sv = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 16; ++k) sv = __builtin_fmaf(a.sk_a[(uint64_t)row * 16 + k], col.w[q][k / 4][k % 4], sv);
+            }
             e = to_f32(ldv<T>(a.mask, i)) *
                 activation_derivative(a.act, sv, to_f32(ldv<T>(a.predrop, i)), to_f32(ldv<T>(a.preact, i)), a.leaky);
         } else {
@@ -657,8 +702,9 @@ __device__ __forceinline__ void err_flat_tail(const ErrArgs &a, uint32_t b, uint
     }
 }
 
-template <typename T, bool FROM_SUM, int B, bool NORM>
+template <typename T, int SRC, int B, bool NORM>
 __global__ void __launch_bounds__(256) error_flat_kernel(ErrArgs a, float *__restrict__ partials, uint32_t per) {
+    constexpr int UB = SRC == 2 ? 2 : ERR_UB;
     const uint32_t n = a.n;
     const uint32_t j = blockIdx.x * 256 + threadIdx.x;
     if ((uint64_t)j * 4 >= (uint64_t)B * n) return;
@@ -669,7 +715,7 @@ __global__ void __launch_bounds__(256) error_flat_kernel(ErrArgs a, float *__res
         fp.r[q] = B == 1 ? 0u : e / n;
         fp.c[q] = e - fp.r[q] * n;
     }
-    ErrCol col{{0, 0, 0, 0}, {0, 0, 0, 0}};
+    ErrCol col{};
     if constexpr (NORM) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) col.nw[q] = a.nw[fp.c[q]];
@@ -678,14 +724,20 @@ __global__ void __launch_bounds__(256) error_flat_kernel(ErrArgs a, float *__res
             for (int q = 0; q < 4; ++q) col.rstd[q] = to_f32(ldv<T>(a.norm_rstd, fp.c[q]));
         }
     }
+    if constexpr (SRC == 2) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) col.w[q][i] = reinterpret_cast<const f32x4 *>(a.sk_w + (uint64_t)fp.c[q] * 16)[i];
+    }
     const uint32_t s_ld = a.s_ld ? a.s_ld : n;
     const uint32_t full = a.rows / B, bands = (a.rows + B - 1) / B;
     const uint32_t b0 = blockIdx.y * per, b1 = min(bands, b0 + per), bf = min(b1, full);
     ErrAcc acc{{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
     uint32_t b = b0;
-    for (; b + ERR_UB <= bf; b += ERR_UB) err_flat_bands<T, FROM_SUM, B, NORM, ERR_UB>(a, b, j, s_ld, fp, col, acc);
-    for (; b < bf; ++b) err_flat_bands<T, FROM_SUM, B, NORM, 1>(a, b, j, s_ld, fp, col, acc);
-    if (b < b1) err_flat_tail<T, FROM_SUM, B>(a, b, s_ld, fp, col, acc);
+    for (; b + UB <= bf; b += UB) err_flat_bands<T, SRC, B, NORM, UB>(a, b, j, s_ld, fp, col, acc);
+    for (; b < bf; ++b) err_flat_bands<T, SRC, B, NORM, 1>(a, b, j, s_ld, fp, col, acc);
+    if (b < b1) err_flat_tail<T, SRC, B>(a, b, s_ld, fp, col, acc);
     float *p = partials + (uint64_t)blockIdx.y * B * 3 * n;
     if constexpr (B == 1) {
         store4<float>(p, 4ull * j, acc.dp);
@@ -915,15 +967,15 @@ uint32_t err_col_splits(uint32_t rows, uint32_t n) {
     return (sp < 1 ? 1 : sp) * band;
 }
 
-template <bool FROM_SUM, typename T, int B>
+template <int SRC, typename T, int B>
 static void launch_error_flat(const ErrArgs &a, float *partials, uint32_t splits, hipStream_t s) {
     const uint32_t S = splits / B;
     const uint32_t per = cdiv(cdiv(a.rows, B), S);
     const dim3 grid(cdiv((uint64_t)B * a.n, 1024), S);
     if (a.norm)
-        hipLaunchKernelGGL((error_flat_kernel<T, FROM_SUM, B, true>), grid, dim3(256), 0, s, a, partials, per);
+        hipLaunchKernelGGL((error_flat_kernel<T, SRC, B, true>), grid, dim3(256), 0, s, a, partials, per);
     else
-        hipLaunchKernelGGL((error_flat_kernel<T, FROM_SUM, B, false>), grid, dim3(256), 0, s, a, partials, per);
+        hipLaunchKernelGGL((error_flat_kernel<T, SRC, B, false>), grid, dim3(256), 0, s, a, partials, per);
 }
 
 // splits: the partial-sum rows, from err_col_splits.
@@ -938,10 +990,25 @@ static hipError_t launch_error_t(const ErrArgs &a0, float *partials, uint32_t sp
     }
     const uint32_t band = err_band(a.n);
     if (splits < band || splits % band) return hipErrorInvalidValue;
+    constexpr int SRC = FROM_SUM ? 1 : 0;
     switch (band) {
-    case 1: launch_error_flat<FROM_SUM, T, 1>(a, partials, splits, s); break;
-    case 2: launch_error_flat<FROM_SUM, T, 2>(a, partials, splits, s); break;
-    default: launch_error_flat<FROM_SUM, T, 4>(a, partials, splits, s); break;
+    case 1: launch_error_flat<SRC, T, 1>(a, partials, splits, s); break;
+    case 2: launch_error_flat<SRC, T, 2>(a, partials, splits, s); break;
+    default: launch_error_flat<SRC, T, 4>(a, partials, splits, s); break;
+    }
+    return hipGetLastError();
+}
+
+template <typename T>
+static hipError_t launch_error_skinny_t(const ErrArgs &a0, float *partials, uint32_t splits, hipStream_t s) {
+    ErrArgs a = a0;
+    a.norm_in = a.norm == 1 ? a.prenorm : a.centered;
+    const uint32_t band = err_band(a.n);
+    if (!err_skinny_ok(a, partials) || splits < band || splits % band) return hipErrorInvalidValue;
+    switch (band) {
+    case 1: launch_error_flat<2, T, 1>(a, partials, splits, s); break;
+    case 2: launch_error_flat<2, T, 2>(a, partials, splits, s); break;
+    default: launch_error_flat<2, T, 4>(a, partials, splits, s); break;
     }
     return hipGetLastError();
 }
@@ -950,6 +1017,56 @@ hipError_t launch_output_error(const ErrArgs &a, float *partials, uint32_t split
     if ((uint64_t)a.rows * a.n == 0) return hipSuccess;
     return a.dtype == 1 ? launch_error_t<false, half_t>(a, partials, splits, s)
                         : launch_error_t<false, float>(a, partials, splits, s);
+}
+
+bool err_skinny_ok(const ErrArgs &a, const float *partials) {
+    return a.n >= 4 && a.sk_a && a.sk_w && a16(a.sk_a) && a16(a.sk_w) && err_aligned(a, true, partials);
+}
+
+// Columns of a skinny operand's fp32 copy.
+constexpr uint32_t SK_COLS = 16;
+
+// dst[r][k] = k < cols ? src[r ld + k] : 0 for k < 16: the next layer's
+// d_prenorm (rows = batch) or weights (rows = n) as the hidden error's skinny
+// operands, rows of A then rows of W in one launch.
+template <typename TA, typename TW>
+__global__ void __launch_bounds__(256) skinny_operands_kernel(const TA *a, uint32_t a_rows, const TW *w, uint32_t w_rows,
+                                                              uint32_t cols, float *a32, float *w32) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    const uint32_t k = (uint32_t)(i % SK_COLS);
+    const uint64_t r = i / SK_COLS;
+    if (r < a_rows) {
+        a32[i] = k < cols ? (float)a[r * cols + k] : 0.0f;
+    } else if (r < (uint64_t)a_rows + w_rows) {
+        const uint64_t rw = r - a_rows;
+        w32[rw * SK_COLS + k] = k < cols ? (float)w[rw * cols + k] : 0.0f;
+    }
+}
+
+hipError_t launch_skinny_operands(uint32_t dtype, const void *a, uint32_t a_rows, const void *w, uint32_t w_rows,
+                                  uint32_t cols, float *a32, float *w32, hipStream_t s) {
+    if (cols == 0 || cols > SK_COLS) return hipErrorInvalidValue;
+    const uint64_t threads = ((uint64_t)a_rows + w_rows) * SK_COLS;
+    if (threads == 0) return hipSuccess;
+    const dim3 grid(cdiv(threads, 256));
+    if (dtype == 1)
+        hipLaunchKernelGGL((skinny_operands_kernel<half_t, half_t>), grid, dim3(256), 0, s,
+                           reinterpret_cast<const half_t *>(a), a_rows, reinterpret_cast<const half_t *>(w), w_rows,
+                           cols, a32, w32);
+    else
+        hipLaunchKernelGGL((skinny_operands_kernel<float, float>), grid, dim3(256), 0, s,
+                           reinterpret_cast<const float *>(a), a_rows, reinterpret_cast<const float *>(w), w_rows,
+                           cols, a32, w32);
+    return hipGetLastError();
+}
+
+hipError_t launch_error_skinny(const ErrArgs &a0, float *partials, uint32_t splits, hipStream_t s) {
+    if ((uint64_t)a0.rows * a0.n == 0) return hipSuccess;
+    ErrArgs a = a0;
+    if (!act_uses_output(a.act)) a.predrop = a.mask;
+    if (!act_uses_input(a.act)) a.preact = a.mask;
+    return a.dtype == 1 ? launch_error_skinny_t<half_t>(a, partials, splits, s)
+                        : launch_error_skinny_t<float>(a, partials, splits, s);
 }
 
 hipError_t launch_error_from_sum(const ErrArgs &a0, float *partials, uint32_t splits, hipStream_t s) {

@@ -7,7 +7,8 @@ GEMM's epilogue computes e = mask * act'(s, ...), grad, the element-local norm
 gradient into d_prenorm / d_prenorm_h / dNorm and each 256-row tile's column
 sums, which the backward that follows takes for db and the norm-parameter
 sums.  Ragged outputs and misaligned buffers take the GEMM + error-kernel pair
-instead; both kinds are here.  Checked against the oracle (fed the device's
+instead, and a next layer of at most 16 outputs the error kernel that forms the
+sum itself; all three kinds are here.  Checked against the oracle (fed the device's
 forward caches) at shapes that select the 256x256 kernel: every norm mode
 (BatchNorm with its per-column rstd), dropout masks, and the parameters after
 backward_hidden (the column sums' only consumer).
@@ -33,7 +34,7 @@ CASES = [
     (4096, 64, 3072, 512, abi.NORM_LAYER, abi.ACT_LEAKY, 0.0, 0),
     (4096, 64, 3072, 512, abi.NORM_BATCH, abi.ACT_TANH, 0.0, 0),   # rstd per column, 1/m
     (4096, 64, 3072, 512, abi.NORM_DISABLED, abi.ACT_SILU, 0.2, 0),
-    (4001, 64, 3001, 13, abi.NORM_LAYER, abi.ACT_LEAKY, 0.0, 0),   # ragged, K 13: GEMM + error kernel
+    (4001, 64, 3001, 13, abi.NORM_LAYER, abi.ACT_LEAKY, 0.0, 0),   # ragged, K 13: error kernel forms the sum
     (4001, 64, 3001, 777, abi.NORM_RMS, abi.ACT_SIGMOID, 0.0, 0),  # ragged: GEMM + error kernel
     (4096, 64, 3072, 512, abi.NORM_RMS, abi.ACT_MISH, 0.0, 1),     # buffers off 16 bytes: GEMM + error kernel
     (4096, 64, 3072, 512, abi.NORM_LAYER, abi.ACT_RELU, 0.0, 3),

@@ -142,8 +142,10 @@ def test_output_error(ctx, half, loss, act, norm):
 # ---------------------------------------------------------------------------------------------
 @pytest.mark.parametrize("half", [False, True])
 @pytest.mark.parametrize("M,K0,N0,N1,norm,act,p", [(128, 64, 96, 80, 0, 6, 0.0), (96, 40, 72, 24, 2, 3, 0.1),
-                                                   (77, 33, 51, 13, 1, 7, 0.0), (256, 128, 256, 192, 0, 2, 0.0)])
+                                                   (77, 33, 51, 13, 1, 7, 0.0), (256, 128, 256, 192, 0, 2, 0.0),
+                                                   (66, 24, 40, 6, 3, 3, 0.0)])
 def test_hidden_error(ctx, half, M, K0, N0, N1, norm, act, p):
+    """Next layers of up to 16 outputs (N1 13, 6) take the error kernel that forms the sum itself."""
     o0, d0 = make_pair(ctx, K0, N0, M, seed=21, half=half, norm=norm, act=act, leaky=0.01, p=p)
     o1, d1 = make_pair(ctx, N0, N1, M, seed=22, half=half, act=abi.ACT_IDENTITY)
     x = inputs(23, M, K0, half)

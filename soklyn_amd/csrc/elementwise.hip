@@ -1321,63 +1321,106 @@ hipError_t launch_dw_reduce_opt(const DwReduceArgs &a0, hipStream_t s) {
 
 // ---- zero-padded fp16 copy (operand staging for the 256x256 GEMM) -----------------------
 // out[r][c] = (r < rows && c < cols) ? in[r ld + c] : 0 for r < rows_p, c < cols_p
-// (cols_p a multiple of 8).  One wave per padded row (grid-stride over rows), lane
-// l writing the 16-byte chunks l, l + 64, ... of it; 32-bit index arithmetic only.
-// Every chunk of a row starts (r ld) mod 8 elements past a 16-byte boundary of the
-// source, so with a 16-byte aligned base (chunks) a chunk is cut out of the two
-// aligned 16-byte source chunks covering it (funnel shifts by that row-wide
-// amount), as long as both lie inside the source's readable elements; element
-// loads otherwise (the row's last partial chunk, the buffer's tail).
+// (cols_p a multiple of 8).  A wave owns a segment of PAD_U x 64 16-byte chunks
+// of one padded row (grid-stride over rows x segments); lane l writes chunks
+// l, l + 64, ... of the segment and issues all of its loads before any store.
+// Every chunk of a source row starts O = (row's first element) mod 8 elements
+// past a 16-byte boundary, so a chunk is cut out of the two aligned 16-byte
+// source chunks covering it; O is one value per row, so pad_row<O> (picked by a
+// wave-uniform switch) does the cut with fixed register selects and 16-bit
+// funnel shifts.  A chunk whose aligned pair would leave the source's readable
+// elements (a row's last partial chunk, the buffer's ends) is read element by
+// element.
+constexpr uint32_t PAD_U = 4;
+template <int O>
+__device__ __forceinline__ void pad_row(const half_t *__restrict__ in, uint64_t rb, int64_t ab, uint32_t cols,
+                                        uint64_t in_elems, u32x4_t *orow, uint32_t g0, uint32_t gpr, uint32_t lane) {
+    // ab: index of the aligned chunk holding element rb, relative to in (may be < 0)
+    u32x4_t lo[PAD_U], hi[PAD_U];
+    bool fast[PAD_U];
+#pragma unroll
+    for (uint32_t u = 0; u < PAD_U; ++u) {
+        const uint32_t g = g0 + u * 64u + lane;
+        const int64_t first = ab + 8ll * g;   // first element of the aligned pair, relative to in
+        fast[u] = g < gpr && 8u * g + 8u <= cols && first >= 0 && (uint64_t)first + (O ? 16u : 8u) <= in_elems;
+        if (fast[u]) {
+            lo[u] = *reinterpret_cast<const u32x4_t *>(in + first);
+            if constexpr (O != 0) hi[u] = *reinterpret_cast<const u32x4_t *>(in + first + 8);
+        }
+    }
+#pragma unroll
+    for (uint32_t u = 0; u < PAD_U; ++u) {
+        const uint32_t g = g0 + u * 64u + lane;
+        if (g >= gpr) continue;
+        u32x4_t v = {0, 0, 0, 0};
+        const uint32_t c = 8u * g;
+        if (fast[u]) {
+            if constexpr (O == 0) {
+                v = lo[u];
+            } else {
+                const uint32_t w[8] = {lo[u].x, lo[u].y, lo[u].z, lo[u].w, hi[u].x, hi[u].y, hi[u].z, hi[u].w};
+                constexpr int WD = O / 2;            // whole dwords to skip
+                constexpr uint32_t BITS = (O & 1) * 16u;
+#pragma unroll
+                for (int d = 0; d < 4; ++d) v[d] = __builtin_amdgcn_alignbit(w[d + WD + 1], w[d + WD], BITS);
+            }
+        } else if (c < cols) {
+            half_t h[8];
+            const half_t *src = in + rb + c;
+#pragma unroll
+            for (uint32_t e = 0; e < 8; ++e) h[e] = c + e < cols ? src[e] : (half_t)0;
+            v = __builtin_bit_cast(u32x4_t, h);
+        }
+        orow[g] = v;
+    }
+}
+
 __global__ void __launch_bounds__(256) pad_h_kernel(const half_t *__restrict__ in, uint32_t rows, uint32_t cols,
                                                     uint32_t ld, half_t *__restrict__ out, uint32_t rows_p,
-                                                    uint32_t cols_p, uint32_t chunks) {
+                                                    uint32_t cols_p) {
     const uint32_t gpr = cols_p / 8;
+    const uint32_t segs = (gpr + PAD_U * 64u - 1) / (PAD_U * 64u);
     const uint64_t in_elems = rows ? (uint64_t)(rows - 1) * ld + cols : 0;   // readable source elements
+    const uint32_t lead = (uint32_t)((reinterpret_cast<uintptr_t>(in) / sizeof(half_t)) & 7u);
     const uint32_t lane = threadIdx.x & 63u;
-    for (uint32_t r = blockIdx.x * 4u + (threadIdx.x >> 6); r < rows_p; r += gridDim.x * 4u) {
+    const uint64_t items = (uint64_t)rows_p * segs;
+    for (uint64_t it = (uint64_t)blockIdx.x * 4u + (threadIdx.x >> 6); it < items; it += (uint64_t)gridDim.x * 4u) {
+        const uint32_t r = (uint32_t)(it / segs), g0 = (uint32_t)(it % segs) * PAD_U * 64u;
         u32x4_t *orow = reinterpret_cast<u32x4_t *>(out + (uint64_t)r * cols_p);
         if (r >= rows) {
-            for (uint32_t g = lane; g < gpr; g += 64u) orow[g] = u32x4_t{0, 0, 0, 0};
+#pragma unroll
+            for (uint32_t u = 0; u < PAD_U; ++u) {
+                const uint32_t g = g0 + u * 64u + lane;
+                if (g < gpr) orow[g] = u32x4_t{0, 0, 0, 0};
+            }
             continue;
         }
-        const uint64_t rb = (uint64_t)r * ld;                   // first source element of the row
-        const uint32_t sh = (uint32_t)(rb & 7u) * 2u;           // its byte offset within an aligned chunk
-        const half_t *abase = in + (rb - (rb & 7u));            // aligned chunk holding it
-        const uint32_t wd = sh >> 2, bits = (sh & 3u) * 8u;     // whole dwords, then 0 or 16 bits
-        for (uint32_t g = lane; g < gpr; g += 64u) {
-            const uint32_t c = g * 8u;
-            u32x4_t v = {0, 0, 0, 0};
-            if (c < cols) {
-                if (chunks && c + 8u <= cols && rb - (rb & 7u) + c + (sh ? 16u : 8u) <= in_elems) {
-                    const u32x4_t lo = *reinterpret_cast<const u32x4_t *>(abase + c);
-                    const u32x4_t hi = sh ? *reinterpret_cast<const u32x4_t *>(abase + c + 8u) : lo;
-                    const uint32_t w[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-#pragma unroll
-                    for (int d = 0; d < 4; ++d) {
-                        const uint32_t x0 = wd == 0 ? w[d] : wd == 1 ? w[d + 1] : wd == 2 ? w[d + 2] : w[d + 3];
-                        const uint32_t x1 = wd == 0 ? w[d + 1] : wd == 1 ? w[d + 2] : wd == 2 ? w[d + 3] : w[d + 4];
-                        v[d] = __builtin_amdgcn_alignbit(x1, x0, bits);   // (x1:x0) >> bits
-                    }
-                } else {
-                    half_t h[8];
-                    const half_t *src = in + rb + c;
-#pragma unroll
-                    for (uint32_t e = 0; e < 8; ++e) h[e] = c + e < cols ? src[e] : (half_t)0;
-                    v = __builtin_bit_cast(u32x4_t, h);
-                }
-            }
-            orow[g] = v;
+        const uint64_t rb = (uint64_t)r * ld;              // first source element of the row
+        const uint32_t o = (uint32_t)((lead + rb) & 7u);   // its offset within an aligned chunk
+        const int64_t ab = (int64_t)rb - o;
+        switch (o) {
+        case 0: pad_row<0>(in, rb, ab, cols, in_elems, orow, g0, gpr, lane); break;
+        case 1: pad_row<1>(in, rb, ab, cols, in_elems, orow, g0, gpr, lane); break;
+        case 2: pad_row<2>(in, rb, ab, cols, in_elems, orow, g0, gpr, lane); break;
+        case 3: pad_row<3>(in, rb, ab, cols, in_elems, orow, g0, gpr, lane); break;
+        case 4: pad_row<4>(in, rb, ab, cols, in_elems, orow, g0, gpr, lane); break;
+        case 5: pad_row<5>(in, rb, ab, cols, in_elems, orow, g0, gpr, lane); break;
+        case 6: pad_row<6>(in, rb, ab, cols, in_elems, orow, g0, gpr, lane); break;
+        default: pad_row<7>(in, rb, ab, cols, in_elems, orow, g0, gpr, lane); break;
         }
     }
 }
 
 hipError_t launch_pad_h(const void *in, uint32_t rows, uint32_t cols, uint32_t ld, void *out, uint32_t rows_p,
                         uint32_t cols_p, hipStream_t s) {
-    if (cols_p % 8 || rows_p < rows || cols_p < cols || !a16(out)) return hipErrorInvalidValue;
+    if (cols_p % 8 || rows_p < rows || cols_p < cols || !a16(out) || (reinterpret_cast<uintptr_t>(in) & 1u))
+        return hipErrorInvalidValue;
     if (rows_p == 0 || cols_p == 0) return hipSuccess;
-    const uint32_t blocks = (rows_p + 3) / 4 < 8192 ? (rows_p + 3) / 4 : 8192;   // 4 rows per block
+    const uint64_t segs = cdiv(cols_p / 8, PAD_U * 64u);
+    const uint64_t waves = (uint64_t)rows_p * segs;
+    const uint32_t blocks = cdiv(waves, 4) < 8192 ? cdiv(waves, 4) : 8192;   // 4 waves per block
     hipLaunchKernelGGL(pad_h_kernel, dim3(blocks), dim3(256), 0, s, reinterpret_cast<const half_t *>(in), rows,
-                       cols, ld, reinterpret_cast<half_t *>(out), rows_p, cols_p, a16(in) ? 1u : 0u);
+                       cols, ld, reinterpret_cast<half_t *>(out), rows_p, cols_p);
     return hipGetLastError();
 }
 

@@ -158,6 +158,11 @@ template <typename T> __global__ void __launch_bounds__(256) norm_rows_kernel(Ro
     }
 }
 
+// 16-byte store of the chunk holding element idx of a T array, with the nontemporal hint.
+template <typename T> __device__ __forceinline__ void nt_store(void *p, uint64_t idx, u32x4_t v) {
+    __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t *>(reinterpret_cast<T *>(p) + idx));
+}
+
 // The same with the row held in registers: each element of prenorm is read
 // once, and every cache write is a 16-byte store when rows are 16-byte aligned
 // (VEC: a thread owns chunks of VW consecutive elements, chunk t + 256 i) or
@@ -259,12 +264,12 @@ template <typename T, bool VEC, int PER> __global__ void __launch_bounds__(256) 
         }
         const uint64_t idx = base + c0;
         if constexpr (VEC) {
-            *reinterpret_cast<u32x4_t *>(reinterpret_cast<T *>(a.centered) + idx) = *reinterpret_cast<u32x4_t *>(cen);
-            *reinterpret_cast<u32x4_t *>(reinterpret_cast<T *>(a.preact) + idx) = *reinterpret_cast<u32x4_t *>(pre);
-            *reinterpret_cast<u32x4_t *>(reinterpret_cast<T *>(a.predrop) + idx) = *reinterpret_cast<u32x4_t *>(pd);
-            *reinterpret_cast<u32x4_t *>(reinterpret_cast<T *>(a.out) + idx) = *reinterpret_cast<u32x4_t *>(ot);
-            if (a.use_dropout)
-                *reinterpret_cast<u32x4_t *>(reinterpret_cast<T *>(a.mask) + idx) = *reinterpret_cast<u32x4_t *>(mk);
+            // nontemporal: five write streams, read again only by later kernels
+            nt_store<T>(a.centered, idx, *reinterpret_cast<u32x4_t *>(cen));
+            nt_store<T>(a.preact, idx, *reinterpret_cast<u32x4_t *>(pre));
+            nt_store<T>(a.predrop, idx, *reinterpret_cast<u32x4_t *>(pd));
+            nt_store<T>(a.out, idx, *reinterpret_cast<u32x4_t *>(ot));
+            if (a.use_dropout) nt_store<T>(a.mask, idx, *reinterpret_cast<u32x4_t *>(mk));
         } else {
             stv<T>(a.centered, idx, cen[0]);
             stv<T>(a.preact, idx, pre[0]);
@@ -380,11 +385,12 @@ template <typename T, int PER> __global__ void __launch_bounds__(256) norm_rows_
         }
         const uint64_t gi = g0 + j;
         if (whole) {
-            reinterpret_cast<G *>(a.centered)[gi] = *reinterpret_cast<G *>(cen);
-            reinterpret_cast<G *>(a.preact)[gi] = *reinterpret_cast<G *>(pre);
-            reinterpret_cast<G *>(a.predrop)[gi] = *reinterpret_cast<G *>(pd);
-            reinterpret_cast<G *>(a.out)[gi] = *reinterpret_cast<G *>(ot);
-            if (a.use_dropout) reinterpret_cast<G *>(a.mask)[gi] = *reinterpret_cast<G *>(mk);
+            // nontemporal: five write streams, read again only by later kernels
+            __builtin_nontemporal_store(*reinterpret_cast<G *>(cen), reinterpret_cast<G *>(a.centered) + gi);
+            __builtin_nontemporal_store(*reinterpret_cast<G *>(pre), reinterpret_cast<G *>(a.preact) + gi);
+            __builtin_nontemporal_store(*reinterpret_cast<G *>(pd), reinterpret_cast<G *>(a.predrop) + gi);
+            __builtin_nontemporal_store(*reinterpret_cast<G *>(ot), reinterpret_cast<G *>(a.out) + gi);
+            if (a.use_dropout) __builtin_nontemporal_store(*reinterpret_cast<G *>(mk), reinterpret_cast<G *>(a.mask) + gi);
         } else {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {

@@ -796,18 +796,20 @@ static int32_t hidden_error_impl(skl_ctx *ctx, const skl_dense_desc *cur, const 
 
     // A next layer of at most 16 outputs: its GEMM would pad k to 128, so the
     // error kernel forms s = next.d_prenorm . next.W^T itself, per element, from
-    // fp32 copies of the two operands padded to 16 columns (same operands as the
+    // copies of the two operands padded to 16 columns (same operands as the
     // GEMM: f16(d_prenorm) and the working W for fp16 blocks).
     if (next->outputs <= 16) {
         uint32_t splits = 0;
         if ((r = ensure_cols(ctx, batch, cur->outputs, &splits))) return r;
-        const size_t a_bytes = ((size_t)batch * 16 * sizeof(float) + 255) & ~(size_t)255;
-        if ((r = ensure_ws(ctx, a_bytes + (size_t)cur->outputs * 16 * sizeof(float)))) return r;
-        a.sk_a = reinterpret_cast<const float *>(ctx->ws);
-        a.sk_w = reinterpret_cast<const float *>(reinterpret_cast<char *>(ctx->ws) + a_bytes);
+        const size_t esz = cur->dtype == SKL_F16 ? 2 : 4;
+        const size_t a_bytes = ((size_t)batch * 16 * esz + 255) & ~(size_t)255;
+        if ((r = ensure_ws(ctx, a_bytes + (size_t)cur->outputs * 16 * esz))) return r;
+        char *a16 = reinterpret_cast<char *>(ctx->ws), *w16 = a16 + a_bytes;
+        a.sk_a = a16;
+        a.sk_w = w16;
         if (err_skinny_ok(a, ctx->cols)) {
-            SKL_TRY(launch_skinny_operands(cur->dtype, next_dp, batch, next->w, cur->outputs, next->outputs,
-                                           const_cast<float *>(a.sk_a), const_cast<float *>(a.sk_w), ctx->stream));
+            SKL_TRY(launch_skinny_operands(cur->dtype, next_dp, batch, next->w, cur->outputs, next->outputs, a16, w16,
+                                           ctx->stream));
             SKL_TRY(launch_error_skinny(a, ctx->cols, splits, ctx->stream));
             record_cols(ctx, cur, batch, splits);
             return SKL_OK;

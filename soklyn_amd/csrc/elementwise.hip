@@ -562,29 +562,56 @@ struct ErrAcc {   // running column sums of a thread's 4 elements
 // SRC: 0 the output layer's loss delta, 1 the hidden error from s in memory,
 // 2 the hidden error with s = A . W^T formed per element (backward.cu:72-77
 // for a next layer of at most 16 outputs: A [rows x 16] and W [n x 16] are
-// fp32 zero-padded copies of the next layer's d_prenorm and weights, so an
-// element's sum is 16 FMAs over k in ascending order, and s never goes
-// through HBM).  With SRC 2 the thread keeps its four columns of W in
-// registers; the n >= 4 it needs puts a chunk's elements in at most two rows.
+// zero-padded T copies of the next layer's d_prenorm (fp16 blocks: its fp16
+// copy) and weights, so an element's sum is an fp32 sum over k in ascending
+// order (skinny_dot), and s never goes through HBM).  With SRC 2 the thread
+// keeps its four columns of W in registers (as T: half the registers of fp32
+// for fp16 blocks); the n >= 4 it needs puts a chunk's elements in at most two
+// rows, and both rows' sums are formed before the element picks its own.
 constexpr int ERR_UB = 4;
 struct FlatPos {
     uint32_t r[4], c[4];
 };
-struct ErrCol {   // per-column operands of the 4 elements
+template <typename T> struct ErrCol {   // per-column operands of the 4 elements
     f32x4 nw, rstd;
-    f32x4 w[4][4];   // SRC 2: W's 16 values of each element's column
+    T w[4][16];   // SRC 2: W's 16 values of each element's column
 };
 
-template <int B> struct SkRows {   // SRC 2: A's rows of a chunk's first and last element
-    f32x4 lo[4], hi[B > 1 ? 4 : 1];
+template <typename T, int B> struct SkRows {   // SRC 2: A's rows of a chunk's first and last element
+    T lo[16], hi[B > 1 ? 16 : 1];
 };
+
+// 16 consecutive T of a 16-byte aligned row.
+template <typename T> __device__ __forceinline__ void load16(T (&dst)[16], const void *p, uint64_t row) {
+    const u32x4_t *src = reinterpret_cast<const u32x4_t *>(reinterpret_cast<const T *>(p) + row * 16);
+    constexpr int W = 16 * sizeof(T) / 16;
+#pragma unroll
+    for (int i = 0; i < W; ++i) reinterpret_cast<u32x4_t *>(dst)[i] = src[i];
+}
+
+// s of one element from its row of A and column of W (16 values each): fp32
+// FMAs over k in ascending order; fp16 operands as 8 v_dot2_f32_f16 on packed
+// pairs (each pair's two exact products added in fp32), so W stays packed.
+__device__ __forceinline__ float skinny_dot(const float (&av)[16], const float (&wv)[16]) {
+    float sv = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) sv = __builtin_fmaf(av[k], wv[k], sv);
+    return sv;
+}
+__device__ __forceinline__ float skinny_dot(const half_t (&av)[16], const half_t (&wv)[16]) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    float sv = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 16; k += 2) sv = __builtin_amdgcn_fdot2(h2{av[k], av[k + 1]}, h2{wv[k], wv[k + 1]}, sv, false);
+    return sv;
+}
 
 template <typename T, int SRC, int B, bool NORM, int UB>
 __device__ __forceinline__ void err_flat_bands(const ErrArgs &a, uint32_t b, uint32_t j, uint32_t s_ld,
-                                               const FlatPos &fp, const ErrCol &col, ErrAcc &acc) {
+                                               const FlatPos &fp, const ErrCol<T> &col, ErrAcc &acc) {
     const uint32_t n = a.n;
     f32x4 x[3][UB], mk[UB], pc[UB], rs[UB];
-    SkRows<B> ar[SRC == 2 ? UB : 1];
+    SkRows<T, B> ar[SRC == 2 ? UB : 1];
 #pragma unroll
     for (int u = 0; u < UB; ++u) {
         const uint32_t row0 = (b + u) * B;
@@ -595,14 +622,8 @@ __device__ __forceinline__ void err_flat_bands(const ErrArgs &a, uint32_t b, uin
             for (int q = 0; q < 4; ++q)
                 x[0][u][q] = a.s[(uint64_t)(row0 + fp.r[q]) * s_ld + fp.c[q]];
         } else if constexpr (SRC == 2) {
-            const f32x4 *lo = reinterpret_cast<const f32x4 *>(a.sk_a + (uint64_t)(row0 + fp.r[0]) * 16);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) ar[u].lo[i] = lo[i];
-            if constexpr (B > 1) {
-                const f32x4 *hi = reinterpret_cast<const f32x4 *>(a.sk_a + (uint64_t)(row0 + fp.r[3]) * 16);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) ar[u].hi[i] = hi[i];
-            }
+            load16<T>(ar[u].lo, a.sk_a, row0 + fp.r[0]);
+            if constexpr (B > 1) load16<T>(ar[u].hi, a.sk_a, row0 + fp.r[3]);
         }
         if constexpr (SRC != 0) {
             x[1][u] = load4<T>(a.predrop, base);
@@ -626,14 +647,11 @@ __device__ __forceinline__ void err_flat_bands(const ErrArgs &a, uint32_t b, uin
         if constexpr (SRC == 2) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const bool lo = B == 1 || fp.r[q] == fp.r[0];
-                float sv = 0.0f;
-#pragma unroll
-                for (int k = 0; k < 16; ++k) {
-                    const float av = lo ? ar[u].lo[k / 4][k % 4] : ar[u].hi[B > 1 ? k / 4 : 0][k % 4];
-                    sv = __builtin_fmaf(av, col.w[q][k / 4][k % 4], sv);
-                }
-                x[0][u][q] = sv;
+                const float slo = skinny_dot(ar[u].lo, col.w[q]);
+                if constexpr (B > 1)
+                    x[0][u][q] = fp.r[q] == fp.r[0] ? slo : skinny_dot(ar[u].hi, col.w[q]);
+                else
+                    x[0][u][q] = slo;
             }
         }
         f32x4 e;
@@ -670,7 +688,7 @@ __device__ __forceinline__ void err_flat_bands(const ErrArgs &a, uint32_t b, uin
 // The last band when rows % B != 0: element by element, rows past the end skipped.
 template <typename T, int SRC, int B>
 __device__ __forceinline__ void err_flat_tail(const ErrArgs &a, uint32_t b, uint32_t s_ld, const FlatPos &fp,
-                                              const ErrCol &col, ErrAcc &acc) {
+                                              const ErrCol<T> &col, ErrAcc &acc) {
     const uint32_t n = a.n;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -683,9 +701,9 @@ __device__ __forceinline__ void err_flat_tail(const ErrArgs &a, uint32_t b, uint
             if constexpr (SRC == 1) {
                 sv = a.s[(uint64_t)row * s_ld + fp.c[q]];
             } else {
-                sv = 0.0f;
-#pragma unroll
-                for (int k = 0; k < 16; ++k) sv = __builtin_fmaf(a.sk_a[(uint64_t)row * 16 + k], col.w[q][k / 4][k % 4], sv);
+                T av[16];
+                load16<T>(av, a.sk_a, row);
+                sv = skinny_dot(av, col.w[q]);
             }
             e = to_f32(ldv<T>(a.mask, i)) *
                 activation_derivative(a.act, sv, to_f32(ldv<T>(a.predrop, i)), to_f32(ldv<T>(a.preact, i)), a.leaky);
@@ -721,7 +739,7 @@ __global__ void __launch_bounds__(256) error_flat_kernel(ErrArgs a, float *__res
         fp.r[q] = B == 1 ? 0u : e / n;
         fp.c[q] = e - fp.r[q] * n;
     }
-    ErrCol col{};
+    ErrCol<T> col{};
     if constexpr (NORM) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) col.nw[q] = a.nw[fp.c[q]];
@@ -732,9 +750,7 @@ __global__ void __launch_bounds__(256) error_flat_kernel(ErrArgs a, float *__res
     }
     if constexpr (SRC == 2) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) col.w[q][i] = reinterpret_cast<const f32x4 *>(a.sk_w + (uint64_t)fp.c[q] * 16)[i];
+        for (int q = 0; q < 4; ++q) load16<T>(col.w[q], a.sk_w, fp.c[q]);
     }
     const uint32_t s_ld = a.s_ld ? a.s_ld : n;
     const uint32_t full = a.rows / B, bands = (a.rows + B - 1) / B;
@@ -1032,37 +1048,37 @@ bool err_skinny_ok(const ErrArgs &a, const float *partials) {
 // Columns of a skinny operand's fp32 copy.
 constexpr uint32_t SK_COLS = 16;
 
-// dst[r][k] = k < cols ? src[r ld + k] : 0 for k < 16: the next layer's
+// dst[r][k] = k < cols ? src[r cols + k] : 0 for k < 16: the next layer's
 // d_prenorm (rows = batch) or weights (rows = n) as the hidden error's skinny
 // operands, rows of A then rows of W in one launch.
-template <typename TA, typename TW>
-__global__ void __launch_bounds__(256) skinny_operands_kernel(const TA *a, uint32_t a_rows, const TW *w, uint32_t w_rows,
-                                                              uint32_t cols, float *a32, float *w32) {
+template <typename T>
+__global__ void __launch_bounds__(256) skinny_operands_kernel(const T *a, uint32_t a_rows, const T *w, uint32_t w_rows,
+                                                              uint32_t cols, T *a16, T *w16) {
     const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
     const uint32_t k = (uint32_t)(i % SK_COLS);
     const uint64_t r = i / SK_COLS;
     if (r < a_rows) {
-        a32[i] = k < cols ? (float)a[r * cols + k] : 0.0f;
+        a16[i] = k < cols ? a[r * cols + k] : (T)0;
     } else if (r < (uint64_t)a_rows + w_rows) {
         const uint64_t rw = r - a_rows;
-        w32[rw * SK_COLS + k] = k < cols ? (float)w[rw * cols + k] : 0.0f;
+        w16[rw * SK_COLS + k] = k < cols ? w[rw * cols + k] : (T)0;
     }
 }
 
 hipError_t launch_skinny_operands(uint32_t dtype, const void *a, uint32_t a_rows, const void *w, uint32_t w_rows,
-                                  uint32_t cols, float *a32, float *w32, hipStream_t s) {
+                                  uint32_t cols, void *a16, void *w16, hipStream_t s) {
     if (cols == 0 || cols > SK_COLS) return hipErrorInvalidValue;
     const uint64_t threads = ((uint64_t)a_rows + w_rows) * SK_COLS;
     if (threads == 0) return hipSuccess;
     const dim3 grid(cdiv(threads, 256));
     if (dtype == 1)
-        hipLaunchKernelGGL((skinny_operands_kernel<half_t, half_t>), grid, dim3(256), 0, s,
-                           reinterpret_cast<const half_t *>(a), a_rows, reinterpret_cast<const half_t *>(w), w_rows,
-                           cols, a32, w32);
+        hipLaunchKernelGGL((skinny_operands_kernel<half_t>), grid, dim3(256), 0, s, reinterpret_cast<const half_t *>(a),
+                           a_rows, reinterpret_cast<const half_t *>(w), w_rows, cols, reinterpret_cast<half_t *>(a16),
+                           reinterpret_cast<half_t *>(w16));
     else
-        hipLaunchKernelGGL((skinny_operands_kernel<float, float>), grid, dim3(256), 0, s,
-                           reinterpret_cast<const float *>(a), a_rows, reinterpret_cast<const float *>(w), w_rows,
-                           cols, a32, w32);
+        hipLaunchKernelGGL((skinny_operands_kernel<float>), grid, dim3(256), 0, s, reinterpret_cast<const float *>(a),
+                           a_rows, reinterpret_cast<const float *>(w), w_rows, cols, reinterpret_cast<float *>(a16),
+                           reinterpret_cast<float *>(w16));
     return hipGetLastError();
 }
 

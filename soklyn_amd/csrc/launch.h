@@ -130,7 +130,7 @@ struct ErrArgs {
     const void *predrop, *mask;                        // error_from_sum
     const void *norm_rstd, *centered, *prenorm;
     const void *norm_in;                               // set by the launchers: prenorm (RMS) or centered
-    const float *sk_a, *sk_w;                          // launch_error_skinny: [rows x 16], [n x 16] fp32
+    const void *sk_a, *sk_w;                           // launch_error_skinny: T [rows x 16], T [n x 16]
     const float *nw;
     float *grad, *d_prenorm, *d_norm_w, *d_norm_b;
     half_t *d_prenorm_h;
@@ -143,12 +143,13 @@ hipError_t launch_error_from_sum(const ErrArgs &a, float *partials, uint32_t spl
 // Partial-sum rows the error kernels write for [rows x n].
 uint32_t err_col_splits(uint32_t rows, uint32_t n);
 // Hidden error from a next layer of at most 16 outputs without the GEMM: s =
-// A . W^T formed inside the error kernel from fp32 zero-padded copies A
-// [rows x 16] (the next layer's d_prenorm) and W [n x 16] (its weights), which
-// launch_skinny_operands writes (dtype 1: fp16 sources, else fp32; cols <= 16).
-// err_skinny_ok: the buffers (16-byte aligned) and n >= 4 fit that kernel.
+// A . W^T formed inside the error kernel from zero-padded copies A [rows x 16]
+// (the next layer's d_prenorm, or its fp16 copy) and W [n x 16] (its weights)
+// in the block's type T, which launch_skinny_operands writes (dtype 1: fp16,
+// else fp32; cols <= 16).  err_skinny_ok: the buffers (16-byte aligned) and
+// n >= 4 fit that kernel.
 hipError_t launch_skinny_operands(uint32_t dtype, const void *a, uint32_t a_rows, const void *w, uint32_t w_rows,
-                                  uint32_t cols, float *a32, float *w32, hipStream_t s);
+                                  uint32_t cols, void *a16, void *w16, hipStream_t s);
 bool err_skinny_ok(const ErrArgs &a, const float *partials);
 hipError_t launch_error_skinny(const ErrArgs &a, float *partials, uint32_t splits, hipStream_t s);
 

@@ -8,6 +8,7 @@
 #include <math.h>
 #include <string.h>
 
+#include <cmath>
 #include <mutex>
 
 #include <hip/hip_runtime.h>
@@ -170,6 +171,7 @@ struct GemmPlan {
     bool skinny;               // N <= 16: the streaming kernels (forward, dW partials)
     bool dma;
     bool pad_a, pad_b;
+    uint32_t tile;             // direct-to-LDS output tile edge (128 or 256)
     uint32_t Mp, Np, Kp;       // dims the kernel runs on
     uint32_t splits;           // split-K slices of a dW (then DwPartial + reduce)
     size_t a_bytes, b_bytes, part_bytes;
@@ -210,8 +212,25 @@ uint32_t dw_dma_splits(uint32_t tiles, uint32_t Kp, uint64_t out_elems) {
     return best;
 }
 
+// Output tile edge for a direct-to-LDS GEMM of Mp x Np (multiples of 256): the
+// one with fewer estimated rounds of work.  A round is 256 workgroups of 256x256
+// (one per CU) or 512 of 128x128 (two per CU); measured on the C3 shapes, the
+// 128x128 kernel does the same work 1.09-1.15x slower (1.23x with the Adam
+// epilogue), so it wins only where the 256x256 grid leaves most of its last
+// round empty (C5's 12544 x 1536 hidden error: 294 tiles, 2 rounds for 1.15
+// of work; 0.151 -> 0.130 ms).  Split-K grids keep 256.
+uint32_t dma_tile(Op op, uint32_t Mp, uint32_t Np, uint32_t splits) {
+    if (const uint32_t f = gemm_dma_tile_forced()) return f;
+    if (splits > 1) return 256;
+    const double t256 = (double)((Mp / 256) * (Np / 256));
+    const double r256 = std::ceil(t256 / 256.0);
+    const double r128 = std::ceil(4.0 * t256 / 512.0) * 0.5 * (op == Op::DwOpt ? 1.25 : 1.15);
+    return r128 < 0.95 * r256 ? 128u : 256u;
+}
+
 GemmPlan plan_gemm(const GemmLaunch &g) {
     GemmPlan p{};
+    p.tile = 256;
     p.splits = 1;
     p.Mp = g.M;
     p.Np = g.N;
@@ -228,6 +247,7 @@ GemmPlan plan_gemm(const GemmLaunch &g) {
     }
     if (g.dtype == SKL_F16 && gemm_dma_enabled() && g.M && g.N && g.K) {
         const uint32_t Mp = round_up(g.M, 256), Np = round_up(g.N, 256), Kp = round_up(g.K, 128);
+        // in units of 256x256 tiles whatever the kernel's tile edge
         const uint32_t tiles = (Mp / 256) * (Np / 256);
         const uint32_t splits = dw && tiles < 160 ? dw_dma_splits(tiles, Kp, (uint64_t)Mp * Np) : 1;
         const bool waste_ok = (uint64_t)Mp * Np <= (uint64_t)g.M * g.N * 3 / 2;
@@ -243,6 +263,7 @@ GemmPlan plan_gemm(const GemmLaunch &g) {
             p.Np = Np;
             p.Kp = Kp;
             p.splits = splits;
+            p.tile = dma_tile(g.op, Mp, Np, splits);
             // A: k-contiguous [M x K] or m-contiguous [K x M]; B likewise with N
             p.pad_a = g.a_kcontig ? !dma_operand_ok(g.A, g.M, g.K, g.lda, 256, 128)
                                   : !dma_operand_ok(g.A, g.K, g.M, g.lda, 128, 256);
@@ -342,6 +363,7 @@ int32_t exec_gemm(skl_ctx *ctx, GemmLaunch g, const GemmPlan &p, char *ws, bool 
         }
         g.mv = full_out ? p.Mp : M;
         g.nv = full_out ? p.Np : N;
+        g.tile = p.tile;
         g.M = p.Mp;
         g.N = p.Np;
         g.K = p.Kp;
@@ -858,7 +880,7 @@ static int32_t hidden_error_impl(skl_ctx *ctx, const skl_dense_desc *cur, const 
         // One kernel, as the reference has it (backward.cu:59-102): the 256x256
         // GEMM's epilogue computes the error from the sum in its accumulators
         // and leaves the column sums of each 256-row tile for cur's backward.
-        const uint32_t tiles_m = plan.Mp / 256;
+        const uint32_t tiles_m = plan.Mp / plan.tile;
         if ((r = ensure_cols_splits(ctx, tiles_m, cur->outputs))) return r;
         if ((r = ensure_ws(ctx, plan.bytes()))) return r;
         e.partials = ctx->cols;

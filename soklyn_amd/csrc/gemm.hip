@@ -321,24 +321,28 @@ template <typename T> struct EpiErrK {
     // in LDS (column 4 lane + j of the tile), then the block adds the waves in
     // order 0..NW-1 and writes the columns < ncols of partials[tm][k].  lds:
     // NW x 3 x 256 floats; the caller has made sure no wave still reads it.
-    template <int NW>
+    template <int NW, int BN>
     __device__ __forceinline__ static void flush(const ErrEpi &e, const Acc &acc, float *lds, uint32_t tid,
                                                  uint32_t tm, uint32_t n0) {
+        // thread (wave, lane) holds the sums of columns 4 (lane % CPL) .. + 3 over
+        // its rows; slot wave RPS + lane / CPL of the NW RPS partials per column
+        constexpr uint32_t CPL = BN / 4, RPS = 64 / CPL, SLOTS = NW * RPS;
         const uint32_t lane = tid & 63u, wave = tid >> 6;
+        const uint32_t slot = wave * RPS + lane / CPL;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const uint32_t c = 4u * lane + j;
-            lds[(wave * 3 + 0) * 256 + c] = acc.dp[j];
-            lds[(wave * 3 + 1) * 256 + c] = acc.nw[j];
-            lds[(wave * 3 + 2) * 256 + c] = acc.nb[j];
+            const uint32_t c = 4u * (lane % CPL) + j;
+            lds[(slot * 3 + 0) * BN + c] = acc.dp[j];
+            lds[(slot * 3 + 1) * BN + c] = acc.nw[j];
+            lds[(slot * 3 + 2) * BN + c] = acc.nb[j];
         }
         __syncthreads();
-        for (uint32_t t = tid; t < 3 * 256; t += 64 * NW) {
-            const uint32_t k = t >> 8, c = t & 255u;
+        for (uint32_t t = tid; t < 3 * BN; t += 64 * NW) {
+            const uint32_t k = t / BN, c = t % BN;
             if ((k > 0 && !e.norm) || n0 + c >= e.ncols) continue;
             float s = 0.0f;
 #pragma unroll
-            for (int w = 0; w < NW; ++w) s += lds[(w * 3 + k) * 256 + c];
+            for (uint32_t w = 0; w < SLOTS; ++w) s += lds[(w * 3 + k) * BN + c];
             e.partials[((uint64_t)tm * 3 + k) * e.ncols + n0 + c] = s;
         }
     }
@@ -454,6 +458,15 @@ bool gemm_dma_enabled() {
     return on;
 }
 
+uint32_t gemm_dma_tile_forced() {
+    static uint32_t t = [] {
+        const char *e = getenv("SOKLYN_GEMM_TILE");
+        const int v = e ? atoi(e) : 0;
+        return v == 128 || v == 256 ? (uint32_t)v : 0u;
+    }();
+    return t;
+}
+
 // Operand layouts the direct-to-LDS kernel is instantiated for: every op with
 // both operands k-contiguous, the forward on W as stored (n-contiguous), and dW
 // on X and dP as stored (m- and n-contiguous).
@@ -517,17 +530,16 @@ bool gemm_direct_ok(const GemmLaunch &g) {
            (g.splits == 0 || g.splits == 1);
 }
 
-// 8 waves per workgroup for every layout (two per SIMD: one issues MFMAs while
-// the other waits on LDS; see gemm_dma.h); the MFMA shape per layout.
-template <class Epi, bool AK, bool BK_>
-static hipError_t run_dma(const GemmLaunch &g, const typename Epi::Params &p, uint32_t splits, uint32_t kps,
-                          hipStream_t s) {
-    constexpr int NW = 8;
-    // v_mfma_f32_16x16x32_f16 when A is k-contiguous (C3 shapes: dX 2% faster back
-    // to back, 5% with a cold last-level cache; forward 2-3%); 32x32x16 when both
-    // operands are transposed (dW), whose 16x16 fragments at 8 waves overflow the
-    // register budget even with A single-buffered
-    constexpr int MI = AK ? 16 : 32;
+// 256x256: 8 waves per workgroup for every layout (two per SIMD: one issues
+// MFMAs while the other waits on LDS; see gemm_dma.h); the MFMA shape per
+// layout: v_mfma_f32_16x16x32_f16 when A is k-contiguous (C3 shapes: dX 2%
+// faster back to back, 5% with a cold last-level cache; forward 2-3%);
+// 32x32x16 when both operands are transposed (dW), whose 16x16 fragments at 8
+// waves overflow the register budget even with A single-buffered.  128x128:
+// 4 waves of 64x64, two workgroups per CU, 16x16x32 for every layout.
+template <class Epi, bool AK, bool BK_, int NW, int MI, int BT>
+static hipError_t run_dma_t(const GemmLaunch &g, const typename Epi::Params &p, uint32_t splits, uint32_t kps,
+                            hipStream_t s) {
     GemmShape sh{};
     sh.M = g.M;
     sh.N = g.N;
@@ -535,20 +547,27 @@ static hipError_t run_dma(const GemmLaunch &g, const typename Epi::Params &p, ui
     sh.lda = g.lda;
     sh.ldb = g.ldb;
     sh.k_per_split = kps;
-    sh.tiles_m = g.M / 256;
-    sh.tiles_n = g.N / 256;
+    sh.tiles_m = g.M / BT;
+    sh.tiles_n = g.N / BT;
     sh.mv = g.mv ? g.mv : g.M;
     sh.nv = g.nv ? g.nv : g.N;
     const dim3 grid(sh.tiles_m * sh.tiles_n, splits);
     const half_t *A = reinterpret_cast<const half_t *>(g.A);
     const half_t *B = reinterpret_cast<const half_t *>(g.B);
     if (dma_full_epilogue(g))
-        launch_timed(g, gemm_dma_kernel<Epi, AK, BK_, NW, false, MI>, grid, dim3(64 * NW), s, sh, A, B, p);
+        launch_timed(g, gemm_dma_kernel<Epi, AK, BK_, NW, false, MI, BT>, grid, dim3(64 * NW), s, sh, A, B, p);
     else if constexpr (EpiSums<Epi>::value)
         return hipErrorInvalidValue;   // whole tiles only (hidden_err_fusable)
     else
-        launch_timed(g, gemm_dma_kernel<Epi, AK, BK_, NW, true, MI>, grid, dim3(64 * NW), s, sh, A, B, p);
+        launch_timed(g, gemm_dma_kernel<Epi, AK, BK_, NW, true, MI, BT>, grid, dim3(64 * NW), s, sh, A, B, p);
     return hipGetLastError();
+}
+
+template <class Epi, bool AK, bool BK_>
+static hipError_t run_dma(const GemmLaunch &g, const typename Epi::Params &p, uint32_t splits, uint32_t kps,
+                          hipStream_t s) {
+    if (g.tile == 128) return run_dma_t<Epi, AK, BK_, 4, 16, 128>(g, p, splits, kps, s);
+    return run_dma_t<Epi, AK, BK_, 8, AK ? 16 : 32, 256>(g, p, splits, kps, s);
 }
 
 hipError_t launch_gemm_dma(const GemmLaunch &g, hipStream_t s) {

@@ -63,16 +63,20 @@
 
 namespace skl {
 
-template <int NW_, int MI_ = 32> struct DmaCfg {
+template <int NW_, int MI_ = 32, int BM_ = 256, int BN_ = 256> struct DmaCfg {
     static_assert(NW_ == 4 || NW_ == 8, "4 or 8 waves");
     static_assert(MI_ == 16 || MI_ == 32, "16x16x32 or 32x32x16 MFMA");
+    static_assert((BM_ == 256 && BN_ == 256) || (BM_ == 128 && BN_ == 128 && NW_ == 4), "tile shapes");
     static constexpr int NW = NW_, MI = MI_;
-    static constexpr int BM = 256, BN = 256, BK = 64, WM = 2, WN = NW / 2, NT = 64 * NW;
+    static constexpr int BM = BM_, BN = BN_, BK = 64, WM = 2, WN = NW / 2, NT = 64 * NW;
     static constexpr int TWM = BM / WM, TWN = BN / WN, MT = TWM / MI, NTL = TWN / MI;
     static constexpr int KSTEP = 512 / MI;         // k per MFMA
     static constexpr int KS = BK / KSTEP;          // k-steps per tile
-    static constexpr int OPB = 256 * BK * 2;       // 32 KB per operand tile
-    static constexpr int STAGEB = 2 * OPB;         // 64 KB per stage
+    static constexpr int OPA = BM * BK * 2;        // bytes per operand tile (32 KB at 256 rows)
+    static constexpr int OPB = BN * BK * 2;
+    static constexpr int STAGEB = OPA + OPB;       // 64 KB per stage at 256 x 256
+    // waves per SIMD: one 256x256 workgroup per CU, or two 128x128 ones
+    static constexpr int WPE = BM == 256 ? NW / 4 : 2;
 };
 
 // One MFMA block; the B fragment (n rows) is the instruction's first operand and
@@ -147,8 +151,8 @@ __device__ __forceinline__ void pin(u32x2 &v) { asm volatile("" : "+v"(v)); }
 // chunks of 8 halves, chunk c of row r stored at slot c ^ ((r >> 1) & 7): any
 // 16 consecutive rows of one chunk column hit 16 distinct 16-byte bank groups.
 // A fragment is one ds_read_b128.
-template <int NW, int NF, int MI = 32> struct OpK {
-    static constexpr int IPO = 32 / NW;   // DMA instructions per tile and wave
+template <int NW, int NF, int MI = 32, int ROWS = 256> struct OpK {
+    static constexpr int IPO = ROWS / 8 / NW;   // DMA instructions per tile and wave
     static constexpr uint32_t CPK = 512 / MI / 8;   // 16-byte chunks of a row per k-step
     struct Frag { u32x4 v[NF]; };
     DmaSrc dma;                       // DMA source of this lane, t = 0, k-tile 0
@@ -206,9 +210,12 @@ template <int NW, int NF, int MI = 32> struct OpK {
 // 4 distinct 64-byte bank windows.  Fragment i of the wave sits 32 rows
 // further on: chunk + 4 i, i.e. the lane's address XOR 64 i (the wave's first
 // row is a multiple of 32 NF, so the chunk bits that i flips start clear).
-template <int NW, int NF, int MI = 32> struct OpN {
-    static constexpr int IPO = 32 / NW;
-    static constexpr uint32_t KSB = 512u * (512 / MI);   // bytes per k-step (KSTEP k-rows)
+template <int NW, int NF, int MI = 32, int COLS = 256> struct OpN {
+    static constexpr uint32_t P = 2u * COLS;             // bytes per LDS k-row
+    static constexpr uint32_t LPR = P / 16u;             // DMA lanes per k-row
+    static constexpr uint32_t RPI = 64u / LPR;           // k-rows per DMA instruction
+    static constexpr int IPO = 64 / RPI / NW;
+    static constexpr uint32_t KSB = P * (512 / MI);      // bytes per k-step (KSTEP k-rows)
     struct Frag { u32x2 v[NF][2]; };
     DmaSrc dma[2];                    // even / odd instructions (their swizzle differs for MI = 16, NW = 4)
     uint32_t step;                    // 2 NW k-rows per DMA instruction of a wave
@@ -223,15 +230,16 @@ template <int NW, int NF, int MI = 32> struct OpN {
 
     __device__ __forceinline__ void init(const half_t *p, uint32_t ld, uint32_t rows, uint32_t mn0, uint32_t wbase,
                                          uint32_t wave, uint32_t lane, uint32_t lds_op_) {
-        // instruction t (q = wave + NW t) fills k-rows 2 q, 2 q + 1; lane -> k-row 2 q + lane / 32,
-        // slot lane % 32; r & 3 does not depend on t (NW is even), (r >> 3) & 1 only on t's parity
+        // instruction t (q = wave + NW t) fills k-rows RPI q .. RPI q + RPI - 1; lane -> k-row
+        // RPI q + lane / LPR, slot lane % LPR; r & 3 does not depend on t (NW is even), (r >> 3) & 1
+        // at most on t's parity
 #pragma unroll
         for (uint32_t t = 0; t < 2; ++t) {
-            const uint32_t r = 2u * (wave + NW * t) + (lane >> 5);
-            const uint32_t cl = (lane & 31u) ^ swz(r);
-            dma[t].init(p, rows * ld * 2u, (2u * wave + (lane >> 5)) * ld * 2u + mn0 * 2u + cl * 16u);
+            const uint32_t r = RPI * (wave + NW * t) + lane / LPR;
+            const uint32_t cl = (lane % LPR) ^ swz(r);
+            dma[t].init(p, rows * ld * 2u, (RPI * wave + lane / LPR) * ld * 2u + mn0 * 2u + cl * 16u);
         }
-        step = 2u * NW * ld * 2u;
+        step = RPI * NW * ld * 2u;
         kstep = 64u * ld * 2u;
         const uint32_t grp = lane >> 4, s = lane & 15u;
         uint32_t row, col;
@@ -242,7 +250,7 @@ template <int NW, int NF, int MI = 32> struct OpN {
             row = 8u * grp + (s >> 2);
             col = wbase + 4u * (s & 3u);                      // wbase % (16 NF) == 0
         }
-        rel = row * 512u + (((col >> 3) ^ swz(row)) * 16u) + (col & 7u) * 2u;
+        rel = row * P + (((col >> 3) ^ swz(row)) * 16u) + (col & 7u) * 2u;
         lds_op = lds_op_;
     }
     __device__ __forceinline__ void issue(int kt, int t, lds_char *dst) const {
@@ -253,7 +261,7 @@ template <int NW, int NF, int MI = 32> struct OpN {
     __device__ __forceinline__ void read_frag(Frag &f, uint32_t stage_off, int ks, int i) const {
         const uint32_t a = lds_op + (rel ^ (2u * MI * i)) + stage_off + KSB * ks;
         ds_read8_tr<0>(f.v[i][0], a);
-        ds_read8_tr<2048>(f.v[i][1], a);
+        ds_read8_tr<4 * P>(f.v[i][1], a);
     }
     __device__ __forceinline__ static u32x4 op(const Frag &f, int i) {
         return u32x4{f.v[i][0].x, f.v[i][0].y, f.v[i][1].x, f.v[i][1].y};
@@ -285,21 +293,22 @@ template <class E> struct EpiSums<E, std::void_t<decltype(E::kColSums)>> {
     typedef typename E::Acc Acc;
 };
 
-template <bool KC, int NW, int NF, int MI> struct DmaOpSel { typedef OpK<NW, NF, MI> type; };
-template <int NW, int NF, int MI> struct DmaOpSel<false, NW, NF, MI> { typedef OpN<NW, NF, MI> type; };
+template <bool KC, int NW, int NF, int MI, int R> struct DmaOpSel { typedef OpK<NW, NF, MI, R> type; };
+template <int NW, int NF, int MI, int R> struct DmaOpSel<false, NW, NF, MI, R> { typedef OpN<NW, NF, MI, R> type; };
 
 // Grid: (tiles, splits).  Split y reduces k in [y k_per_split, (y + 1) k_per_split)
 // (k_per_split a multiple of 128; the last split may be shorter, also a
 // multiple of 128).  EDGE: the operands are zero-padded copies whose M, N
 // extend past the real output [mv x nv]; the epilogue then goes element by
 // element through Epi::apply with those bounds (any leading dimension).
-template <class Epi, bool A_KC, bool B_KC, int NW, bool EDGE, int MI = 32>
-__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4)))
+template <class Epi, bool A_KC, bool B_KC, int NW, bool EDGE, int MI = 32, int BT = 256>
+__global__ void __launch_bounds__(64 * NW)
+    __attribute__((amdgpu_waves_per_eu(DmaCfg<NW, MI, BT, BT>::WPE, DmaCfg<NW, MI, BT, BT>::WPE)))
     gemm_dma_kernel(GemmShape sh, const half_t *__restrict__ A, const half_t *__restrict__ B,
                     typename Epi::Params ep) {
-    typedef DmaCfg<NW, MI> C;
-    typedef typename DmaOpSel<A_KC, NW, C::MT, MI>::type OA;
-    typedef typename DmaOpSel<B_KC, NW, C::NTL, MI>::type OB;
+    typedef DmaCfg<NW, MI, BT, BT> C;
+    typedef typename DmaOpSel<A_KC, NW, C::MT, MI, C::BM>::type OA;
+    typedef typename DmaOpSel<B_KC, NW, C::NTL, MI, C::BN>::type OB;
     typedef DmaMma<MI> MM;
     static_assert(C::KS % 2 == 0, "k-steps alternate between two fragment sets");
     constexpr int EPITCH = C::BN + 4;
@@ -328,14 +337,14 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
     OA oa;
     OB ob;
     oa.init(A, sh.lda, A_KC ? sh.M : sh.K, m0, wm * C::TWM, wave, lane, lds0);
-    ob.init(B, sh.ldb, B_KC ? sh.N : sh.K, n0, wn * C::TWN, wave, lane, lds0 + C::OPB);
+    ob.init(B, sh.ldb, B_KC ? sh.N : sh.K, n0, wn * C::TWN, wave, lane, lds0 + C::OPA);
 
     auto issue = [&](int kt, int stage) {
         lds_char *st = lsm + stage * C::STAGEB + wave * 1024u;
 #pragma unroll
         for (int t = 0; t < OA::IPO; ++t) oa.issue(kt, t, st);
 #pragma unroll
-        for (int t = 0; t < OB::IPO; ++t) ob.issue(kt, t, st + C::OPB);
+        for (int t = 0; t < OB::IPO; ++t) ob.issue(kt, t, st + C::OPA);
     };
 
     typename MM::Acc acc[C::MT][C::NTL];
@@ -372,7 +381,7 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
         if (q < OA::IPO)
             oa.issue(kt, q, st);
         else
-            ob.issue(kt, q - OA::IPO, st + C::OPB);
+            ob.issue(kt, q - OA::IPO, st + C::OPA);
     };
     // The fragment set `cur` is complete (its reads were the only LDS reads
     // pending), and no MFMA on it may be scheduled above this point.
@@ -512,11 +521,12 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
     wait_lgkmcnt<0>();
     __syncthreads();
 
-    // Epilogue through LDS: two passes of 128 rows (rows of accumulator block
-    // i = pass * MTP + ii of both wave rows).  A thread owns the fixed 4-column
-    // group c of the tile (a wave covers one whole 256-column row per step, so
-    // LDS reads and global accesses are contiguous) and walks rows
-    // wave, wave + NW, ...; the per-element loads of EPI_BATCH rows are issued
+    // Epilogue through LDS: passes of 128 rows (rows of accumulator block
+    // i = pass * MTP + ii of both wave rows; two passes at 256 x 256, one at
+    // 128 x 128).  A thread owns the fixed 4-column group c of the tile (a wave
+    // covers RPS whole rows per step: one of 256 columns or two of 128, so LDS
+    // reads and global accesses are contiguous) and walks its rows; the
+    // per-element loads of EPI_BATCH rows are issued
     // before any of them is consumed, so the loop keeps that many in flight
     // instead of paying one memory latency per row (4 rows for large per-row
     // operand sets at 8 waves, whose 256-register budget they would overflow).
@@ -524,21 +534,23 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
     constexpr bool SUMS = EpiSums<Epi>::value;
     static_assert(!(SUMS && EDGE), "column-sum epilogues run on whole tiles only");
     typename EpiSums<Epi>::Acc csum{};
-    constexpr int ROWS_PER_THREAD = PROWS / NW;
+    constexpr int CPL = C::BN / 4;                 // 4-column groups per row
+    constexpr int RPS = 64 / CPL;                  // rows per wave step
+    constexpr int ROWS_PER_THREAD = PROWS / (NW * RPS);
     static_assert(ROWS_PER_THREAD % EPI_BATCH == 0, "epilogue batch");
-    static_assert(C::BN / 4 == 64, "one wave per 256-column row");
     float *E = reinterpret_cast<float *>(smem);
-    const uint32_t c = lane * 4u;
+    const uint32_t c = (lane % CPL) * 4u, sub = lane / CPL;
     GemmShape shv = sh;   // EDGE: bounds of the real output
     shv.M = sh.mv;
     shv.N = sh.nv;
     const typename Epi::Params eps = Epi::at_split(ep, split);
     const typename Epi::Col col = EDGE ? typename Epi::Col{} : Epi::column(eps, n0 + c);
     // EDGE: lane l's columns n0 + l + 64 q, their per-column operands loaded once
-    typename Epi::Col1 col1[4];
+    constexpr int EQ = C::BN / 64;
+    typename Epi::Col1 col1[EQ];
     if constexpr (EDGE) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < EQ; ++q) {
             const uint32_t n = n0 + lane + 64u * q;
             col1[q] = n < shv.N ? Epi::column1(ep, n) : typename Epi::Col1{};
         }
@@ -568,19 +580,19 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
         }
         lds_barrier();
         if constexpr (EDGE) {
-            // element by element, lane l taking columns l, l + 64, l + 128, l + 192
-            // of the row: each store instruction covers 64 consecutive columns
+            // element by element, lane l taking columns l, l + 64, ... of the
+            // row: each store instruction covers 64 consecutive columns
             // whatever the output's alignment; the per-column operands (bias)
             // were loaded above, so a row is stores only (plus dW's per-element
             // optimiser state)
 #pragma unroll 2
-            for (int b = 0; b < ROWS_PER_THREAD; ++b) {
+            for (int b = 0; b < PROWS / NW; ++b) {
                 const uint32_t r = wave + (uint32_t)NW * b;
                 const uint32_t wmi = r / RPP, rr = r % RPP;
                 const uint32_t m = m0 + wmi * C::TWM + pass * RPP + rr;
                 if (m >= shv.M) continue;
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
+                for (int q = 0; q < EQ; ++q) {
                     const uint32_t n = n0 + lane + 64u * q;
                     if (n >= shv.N) break;
                     Epi::apply1(ep, m, n, E[r * EPITCH + lane + 64u * q], col1[q], split);
@@ -596,14 +608,14 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
 #pragma unroll
             for (int u = 0; u < EPI_BATCH; ++u) {
                 // E row r holds tile row wmi * TWM + pass * RPP + rr
-                const uint32_t r = wave + (uint32_t)NW * (b + u);
+                const uint32_t r = (wave + (uint32_t)NW * (b + u)) * RPS + sub;
                 const uint32_t wmi = r / RPP, rr = r % RPP;
                 mrow[u] = m0 + wmi * C::TWM + pass * RPP + rr;
                 Epi::load(eps, (uint64_t)mrow[u] * Epi::ldc(eps) + n0 + c, mrow[u], pre[u]);
             }
 #pragma unroll
             for (int u = 0; u < EPI_BATCH; ++u) {
-                const uint32_t r = wave + (uint32_t)NW * (b + u);
+                const uint32_t r = (wave + (uint32_t)NW * (b + u)) * RPS + sub;
                 const floatx4 v = *reinterpret_cast<const floatx4 *>(E + r * EPITCH + c);
                 if constexpr (SUMS)
                     Epi::finish(eps, (uint64_t)mrow[u] * Epi::ldc(eps) + n0 + c, mrow[u], n0 + c, v, col, pre[u],
@@ -615,9 +627,9 @@ __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(NW
         if (pass + 1 < C::TWM / RPP) lds_barrier();   // E is rewritten by the next pass
     }
     if constexpr (SUMS) {
-        static_assert(NW * 3 * 256 * 4 <= EPI_BYTES, "column-sum staging fits the epilogue's LDS");
+        static_assert(NW * RPS * 3 * C::BN * 4 <= EPI_BYTES, "column-sum staging fits the epilogue's LDS");
         lds_barrier();   // every wave is done reading E
-        Epi::template flush<NW>(eps, csum, E, tid, tm, n0);
+        Epi::template flush<NW, C::BN>(eps, csum, E, tid, tm, n0);
     }
 }
 

@@ -69,6 +69,7 @@ struct GemmLaunch {
     bool a_kcontig, b_kcontig;
     const void *A, *B;
     uint32_t splits;      // split-K factor (DwPartial only; 1 otherwise)
+    uint32_t tile;        // direct-to-LDS kernel: 128 (4 waves, two workgroups per CU) or 256 (0 = 256)
     uint32_t mv, nv;      // real output extent when A / B are zero-padded copies (0 = M, N)
     Op op;
     FwdEpi fwd;
@@ -95,6 +96,9 @@ hipError_t launch_skinny_dw(const GemmLaunch &g, float *partials, uint32_t slice
 hipError_t launch_gemm_dma(const GemmLaunch &g, hipStream_t stream);
 bool gemm_dma_shape_ok(const GemmLaunch &g);
 bool gemm_dma_enabled();
+// Output tile edge of the direct-to-LDS kernel forced by SOKLYN_GEMM_TILE (128 or
+// 256), or 0: the planner picks per GEMM.
+uint32_t gemm_dma_tile_forced();
 // Number of split-K slices launch_gemm_dma makes when asked for `splits`.
 uint32_t gemm_dma_splits(uint32_t K, uint32_t splits);
 // Number of output tiles the launcher would use (for split-K sizing).

@@ -8,8 +8,9 @@ Every step goes through the C ABI (libsoklyn_hip.so) with its inputs resident in
 Single blocks (c3 = BASELINE config 3, the headline; c2 = config 2), one step =
   1. skl_dense_forward        Z = X.W + b, act           (GEMM, fused epilogue)
   2. skl_dense_error_from_sum dP = dY * act'(Z)           (element-wise + column sums)
-  3. skl_dense_backward       dW = X^T.dP + optimiser on W, db + optimiser on b
-  4. skl_dense_input_grad     dX = dP.W^T (updated W, src/ffn.rs:142-163 order)
+  3. skl_dense_input_grad     dX = dP.W^T with the forward's W (the backward of a
+                              single block, before its optimiser step)
+  4. skl_dense_backward       dW = X^T.dP + optimiser on W, db + optimiser on b
   algorithmic work = 3 GEMMs x 2*M*K*N flops.
 MLPs (c4 = config 4, c5 = config 5), one step = FeedForwardNetwork's train step
 (src/ffn.rs:40-166): forward of every layer, output error, backward of the output
@@ -168,8 +169,8 @@ def cpu_baseline_block(cfg, rows: int, reps: int = 3):
         t0 = time.perf_counter()
         ob.forward(x, rows)
         ob.error_from_sum(s, rows)
-        ob.backward(x, opt, opt, rows, 1e-3, 3.4e38, step)
         ob.input_grad(rows)
+        ob.backward(x, opt, opt, rows, 1e-3, 3.4e38, step)
         return time.perf_counter() - t0
 
     one(1)
@@ -230,8 +231,8 @@ def timing_events(n):
 
 
 class BlockBench:
-    """Single DenseBlock: forward -> error_from_sum -> backward -> input_grad."""
-    calls = ("forward", "error_from_sum", "backward", "input_grad")
+    """Single DenseBlock: forward -> error_from_sum -> input_grad -> backward."""
+    calls = ("forward", "error_from_sum", "input_grad", "backward")
     # GEMM kernels timed alone (the roofline candidates): forward (+bias, act), dW (+ the
     # optimiser step on W in its epilogue) and dX
     gemms = ("forward_gemm", "dw_gemm", "dx_gemm")
@@ -272,8 +273,8 @@ class BlockBench:
         self.step_no += 1
         b, M = self.blk, self.M
         fns = (lambda: b.forward(self.x, M), lambda: b.error_from_sum(self.dy, M),
-               lambda: b.backward(self.x, self.tc, self.step_no), lambda: b.input_grad(M, self.dx))
-        gemm_of = {0: 0, 2: 1, 3: 2}
+               lambda: b.input_grad(M, self.dx), lambda: b.backward(self.x, self.tc, self.step_no))
+        gemm_of = {0: 0, 2: 2, 3: 1}   # call index -> index in self.gemms
         for i, fn in enumerate(fns):
             if gev is not None and i in gemm_of:
                 self.ctx.time_next_gemm(*gev[gemm_of[i]])

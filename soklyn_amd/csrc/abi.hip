@@ -146,6 +146,11 @@ void record_cols(skl_ctx *ctx, const skl_dense_desc *b, uint32_t rows, uint32_t 
     c.valid = true;
 }
 
+bool overlaps(const void *a, size_t an, const void *b, size_t bn) {
+    const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+    return a && b && x < y + bn && y < x + an;
+}
+
 bool cols_match(const skl_ctx *ctx, const skl_dense_desc *b, uint32_t rows) {
     const ColSums &c = ctx->cs;
     return c.valid && c.call + 1 >= ctx->calls && c.dp == b->d_prenorm && c.rows == rows && c.n == b->outputs &&
@@ -1150,6 +1155,22 @@ int32_t skl_dense_input_grad(skl_ctx *ctx, const skl_dense_desc *b, uint32_t bat
     const GemmPlan plan = plan_gemm(g);
     if ((r = ensure_ws(ctx, plan.bytes()))) return r;
     if ((r = exec_gemm(ctx, g, plan, reinterpret_cast<char *>(ctx->ws)))) return r;
+    // dX reads d_prenorm (or its fp16 copy) and W and writes dx only: column sums
+    // that the error call just before left stay valid for the backward after
+    // this call (a single block's dX before its optimiser step), unless dx
+    // overlaps a buffer they were summed from
+    ColSums &c = ctx->cs;
+    if (c.valid && c.call + 1 >= ctx->calls) {
+        const size_t dx_bytes = (size_t)batch * b->inputs * sizeof(float);
+        const size_t buf_bytes = (size_t)c.rows * c.n * sizeof(float);
+        const bool hit = overlaps(dx, dx_bytes, c.dp, buf_bytes) ||
+                         (c.norm != SKL_NORM_DISABLED &&
+                          (overlaps(dx, dx_bytes, c.dnw, buf_bytes) || overlaps(dx, dx_bytes, c.dnb, buf_bytes)));
+        if (hit)
+            c.valid = false;
+        else
+            c.call = ctx->calls;
+    }
     return finish(ctx);
 }
 

@@ -66,12 +66,13 @@ def single_block_step(ctx, M, K, N, half, act, opt_o, opt_d, lr):
         check(n, db.get(n), getattr(ob, n), tol)
     sync_caches(ob, db)
     print("backward", flush=True)
+    # a single block: dX with the forward's W, then the optimiser step
     ob.error_from_sum(s, M)
-    ob.backward(x, opt_o, opt_o, M, lr, 3.4e38, 1)
     dx_ref = ob.input_grad(M)
+    ob.backward(x, opt_o, opt_o, M, lr, 3.4e38, 1)
     db.error_from_sum(torch.from_numpy(s).cuda(), M)
-    db.backward(xd, abi.train_ctx(opt_d, opt_d, M, lr), 1)
     dx = db.input_grad(M)
+    db.backward(xd, abi.train_ctx(opt_d, opt_d, M, lr), 1)
     torch.cuda.synchronize()
     return ob, db, dx.cpu().numpy(), dx_ref, w
 

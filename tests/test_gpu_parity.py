@@ -202,9 +202,19 @@ def _run_backward(ctx, half, M, K, N, norm, opt_kind, step=1, regularisation=0, 
     s = (rng(43).standard_normal((M, N)) * 512).astype(np.float32)
     ob.error_from_sum(s, M)
     db.error_from_sum(torch.from_numpy(s).cuda(), M)
-    if call_between:
-        # any entry point between the error and the backward call: the backward then sums
-        # d_prenorm / dNorm over the rows itself instead of using the error call's sums
+    if call_between == "input_grad":
+        # dX between the error and the backward call (a single block's order): it leaves
+        # d_prenorm / dNorm alone, so the backward keeps the error call's column sums
+        ob.input_grad(M)
+        db.input_grad(M)
+    elif call_between == "input_grad_into_d_prenorm":
+        # dx written over d_prenorm (K == N): the backward must sum the overwritten
+        # d_prenorm, as the reference's backward reads whatever the buffer holds
+        ob.d_prenorm[:M] = ob.input_grad(M)
+        db.input_grad(M, out=db.d_prenorm[:M])
+    elif call_between:
+        # any other entry point between the error and the backward call: the backward then
+        # sums d_prenorm / dNorm over the rows itself instead of using the error call's sums
         ctx.synchronize()
     if opt_kind == abi.OPT_SGD:
         oo, do = O.Optimiser.sgd(0.0), abi.sgd(0.0)
@@ -238,11 +248,13 @@ def test_backward_sgd(ctx, half, M, K, N, norm):
 
 @pytest.mark.parametrize("half", [False, True])
 @pytest.mark.parametrize("norm", [0, 1, 2])
-@pytest.mark.parametrize("call_between", [False, True])
+@pytest.mark.parametrize("call_between", [False, True, "input_grad", "input_grad_into_d_prenorm"])
 def test_backward_column_sums_from_error_call_or_recomputed(ctx, half, norm, call_between):
     """db and the dNorm sums come from the error call's own pass over the rows when the
-    backward directly follows it, and are recomputed otherwise; both match the oracle."""
-    ob, db = _run_backward(ctx, half, 320, 96, 200, norm, abi.OPT_SGD, call_between=call_between)
+    backward directly follows it (or follows a dX call that leaves the buffers alone), and
+    are recomputed otherwise; all match the oracle."""
+    K = 200 if call_between == "input_grad_into_d_prenorm" else 96
+    ob, db = _run_backward(ctx, half, 320, K, 200, norm, abi.OPT_SGD, call_between=call_between)
     tol = FP16_TOL if half else FP32_TOL
     check("dv_b (= db)", db.get("dv_b"), ob.dv_b, tol)
     if norm:

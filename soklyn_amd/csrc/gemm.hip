@@ -75,6 +75,56 @@ template <typename T> struct EpiFwdK {
             store4_nt<T>(e.out, idx, a);
         }
     }
+    // 8 consecutive columns (fp16 outputs: 16-byte stores)
+    static constexpr int kVec = sizeof(T) == 2 ? 8 : 4;
+    struct Col8 { f32x4 lo, hi; };
+    __device__ __forceinline__ static Col8 column8(const FwdEpi &e, uint32_t n) {
+        Col8 c;
+        c.lo = e.bias ? load4<T>(e.bias, n) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        c.hi = e.bias ? load4<T>(e.bias, n + 4) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        return c;
+    }
+    __device__ __forceinline__ static void st8(void *p, uint64_t idx, f32x4 lo, f32x4 hi) {
+        const half_t h[8] = {(half_t)lo[0], (half_t)lo[1], (half_t)lo[2], (half_t)lo[3],
+                             (half_t)hi[0], (half_t)hi[1], (half_t)hi[2], (half_t)hi[3]};
+        __builtin_nontemporal_store(*reinterpret_cast<const u32x4 *>(h),
+                                    reinterpret_cast<u32x4 *>(reinterpret_cast<half_t *>(p) + idx));
+    }
+    __device__ __forceinline__ static void finish8(const FwdEpi &e, uint64_t idx, uint32_t m, uint32_t n, floatx4 v0,
+                                                   floatx4 v1, const Col8 &col) {
+        f32x4 z0 = v0, z1 = v1;
+        if (e.bias) {
+            z0 = z0 + col.lo;
+            z1 = z1 + col.hi;
+        }
+        st8(e.z_out, idx, z0, z1);
+        if (!e.fuse_act) return;
+        const f32x4 t0 = round4<T>(z0), t1 = round4<T>(z1);
+        f32x4 a0, a1;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            a0[j] = activation(e.act, t0[j], e.leaky);
+            a1[j] = activation(e.act, t1[j], e.leaky);
+        }
+        st8(e.predrop, idx, a0, a1);
+        if (e.use_dropout) {
+            const float scale = 1.0f / (1.0f - e.p);
+            f32x4 m0, m1, o0, o1;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const bool k0 = dropout_u(n + j, m, e.seed + m * 7u) >= e.p;
+                const bool k1 = dropout_u(n + 4 + j, m, e.seed + m * 7u) >= e.p;
+                m0[j] = k0 ? scale : 0.0f;
+                o0[j] = k0 ? a0[j] * scale : 0.0f;
+                m1[j] = k1 ? scale : 0.0f;
+                o1[j] = k1 ? a1[j] * scale : 0.0f;
+            }
+            st8(e.mask, idx, m0, m1);
+            st8(e.out, idx, o0, o1);
+        } else {
+            st8(e.out, idx, a0, a1);
+        }
+    }
     // one element (ragged tiles): per-column operands loaded once per column
     struct Col1 { float bias; };
     __device__ __forceinline__ static Col1 column1(const FwdEpi &e, uint32_t n) {

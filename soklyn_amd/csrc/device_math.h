@@ -67,8 +67,35 @@ __device__ __forceinline__ float sigmoid_fast(float x) {
     return __builtin_amdgcn_rcpf(1.0f + __expf(-x));
 }
 
-// util.cu:8-47
-__device__ __forceinline__ float activation(uint32_t act, float x, float leaky) {
+// Mish for fp16 blocks (util.cu:28-39) and its derivative (util.cu:75-87) from
+// one hardware exp and reciprocal per element: with u = e^x and n = u (u + 2),
+// tanh(softplus(x)) = n / (n + 2) and 1 - tanh^2 = 4 (n + 1) / (n + 2)^2.  Above
+// x = 20 the reference takes softplus = x, so tanh is 1 (the derivative 1) until
+// e^x overflows, where its result is NaN; both kept here.  Elsewhere the two
+// forms differ by a few fp32 ulp, except as x -> -inf, where the reference's
+// e^sp - e^-sp cancels (relative error ~1e-7 / e^x): far below what an fp16
+// result resolves.  fp32 blocks keep the reference's form.
+constexpr float kExpOverflow = 88.72283935546875f;   // least float whose e^x rounds to +inf
+__device__ __forceinline__ float mish_fast(float x) {
+    const float u = __expf(x);
+    const float n = u * (u + 2.0f);
+    const float t = n * __builtin_amdgcn_rcpf(n + 2.0f);
+    if (x > 20.0f) return x >= kExpOverflow ? __builtin_nanf("") : x;
+    return x * t;
+}
+__device__ __forceinline__ float mish_slope_fast(float x) {
+    const float u = __expf(x);
+    const float n = u * (u + 2.0f);
+    const float r = __builtin_amdgcn_rcpf(n + 2.0f);
+    const float t = n * r;
+    const float sech2 = (4.0f * (n + 1.0f)) * r * r;
+    const float sig = u * __builtin_amdgcn_rcpf(1.0f + u);
+    if (x > 20.0f) return x >= kExpOverflow ? __builtin_nanf("") : 1.0f;
+    return t + x * sig * sech2;
+}
+
+// util.cu:8-47; T is the block's element type (selects the Mish form above).
+template <typename T> __device__ __forceinline__ float activation(uint32_t act, float x, float leaky) {
     switch (act) {
     case 1: return sigmoid_fast(x);
     case 2: return fmaxf(0.0f, x);
@@ -76,6 +103,7 @@ __device__ __forceinline__ float activation(uint32_t act, float x, float leaky) 
     case 4: return tanhf(x);
     case 6: return x * sigmoid_fast(x);
     case 7: {
+        if constexpr (sizeof(T) == 2) return mish_fast(x);
         const float e_x = expf(x);
         const float sp = x > 20.0f ? x : logf(1.0f + e_x);   // softplus with the reference cutoff
         const float e_sp = expf(sp);
@@ -87,6 +115,7 @@ __device__ __forceinline__ float activation(uint32_t act, float x, float leaky) 
 }
 
 // util.cu:49-93 (ReLU / LeakyReLU test the post-activation value out_v)
+template <typename T>
 __device__ __forceinline__ float activation_derivative(uint32_t act, float err, float out_v, float in_x,
                                                        float leaky) {
     switch (act) {
@@ -99,6 +128,7 @@ __device__ __forceinline__ float activation_derivative(uint32_t act, float err, 
         return err * (sig + out_v * (1.0f - sig));
     }
     case 7: {
+        if constexpr (sizeof(T) == 2) return err * mish_slope_fast(in_x);
         const float e_x = expf(in_x);
         const float sp = in_x > 20.0f ? in_x : logf(1.0f + e_x);
         const float e_sp = expf(sp);

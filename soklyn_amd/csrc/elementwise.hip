@@ -92,7 +92,7 @@ __device__ __forceinline__ float block_max256(float v, float *red) {
 // act + dropout of one element (forward.cu:139-160), input = rounded preact.
 template <typename T>
 __device__ __forceinline__ void act_dropout(const RowNormArgs &a, uint64_t idx, uint32_t row, uint32_t col, T pre) {
-    const float v = activation(a.act, to_f32(pre), a.leaky);
+    const float v = activation<T>(a.act, to_f32(pre), a.leaky);
     stv<T>(a.predrop, idx, from_f32<T>(v));
     if (a.use_dropout) {
         if (dropout_u(col, row, a.seed + row * 7u) >= a.p) {
@@ -252,7 +252,7 @@ template <typename T, bool VEC, int PER> __global__ void __launch_bounds__(256) 
                 p = from_f32<T>(fmaf(v * rstd32, to_f32(g[e]), to_f32(bb[e])));
             }
             pre[e] = p;
-            const float act = activation(a.act, to_f32(p), a.leaky);
+            const float act = activation<T>(a.act, to_f32(p), a.leaky);
             pd[e] = from_f32<T>(act);
             if (a.use_dropout) {
                 const bool keep = dropout_u(c0 + e, row, a.seed + row * 7u) >= a.p;
@@ -373,7 +373,7 @@ template <typename T, int PER> __global__ void __launch_bounds__(256) norm_rows_
                 p = from_f32<T>(fmaf(v * rstd32, gw, gb));
             }
             pre[e] = p;
-            const float act = activation(a.act, to_f32(p), a.leaky);
+            const float act = activation<T>(a.act, to_f32(p), a.leaky);
             pd[e] = from_f32<T>(act);
             if (a.use_dropout) {
                 const bool keep = dropout_u(cc, row, a.seed + row * 7u) >= a.p;
@@ -515,9 +515,9 @@ hipError_t launch_softmax(uint32_t dtype, void *out, uint32_t rows, uint32_t n, 
 
 // ---- error kernels ------------------------------------------------------------------
 // Loss delta of one element (backward.cu:24-45).
-__device__ __forceinline__ float output_err1(const ErrArgs &a, float out, float tg, float pre) {
-    const float o = activation(a.act, out, a.leaky);
-    if (a.loss == 0) return activation_derivative(a.act, o - tg, o, pre, a.leaky);
+template <typename T> __device__ __forceinline__ float output_err1(const ErrArgs &a, float out, float tg, float pre) {
+    const float o = activation<T>(a.act, out, a.leaky);
+    if (a.loss == 0) return activation_derivative<T>(a.act, o - tg, o, pre, a.leaky);
     if ((a.loss == 1 && a.act == 5) || (a.loss == 2 && a.act == 1)) return o - tg;
     return 0.0f;
 }
@@ -658,9 +658,9 @@ __device__ __forceinline__ void err_flat_bands(const ErrArgs &a, uint32_t b, uin
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             if constexpr (SRC != 0)
-                e[q] = mk[u][q] * activation_derivative(a.act, x[0][u][q], x[1][u][q], x[2][u][q], a.leaky);
+                e[q] = mk[u][q] * activation_derivative<T>(a.act, x[0][u][q], x[1][u][q], x[2][u][q], a.leaky);
             else
-                e[q] = output_err1(a, x[0][u][q], x[1][u][q], x[2][u][q]);
+                e[q] = output_err1<T>(a, x[0][u][q], x[1][u][q], x[2][u][q]);
         }
         store4<float>(a.grad, base, e);
         f32x4 dp = e * a.loss_scale;
@@ -706,9 +706,9 @@ __device__ __forceinline__ void err_flat_tail(const ErrArgs &a, uint32_t b, uint
                 sv = skinny_dot(av, col.w[q]);
             }
             e = to_f32(ldv<T>(a.mask, i)) *
-                activation_derivative(a.act, sv, to_f32(ldv<T>(a.predrop, i)), to_f32(ldv<T>(a.preact, i)), a.leaky);
+                activation_derivative<T>(a.act, sv, to_f32(ldv<T>(a.predrop, i)), to_f32(ldv<T>(a.preact, i)), a.leaky);
         } else {
-            e = output_err1(a, to_f32(ldv<T>(a.out, i)), to_f32(ldv<T>(a.target, i)), to_f32(ldv<T>(a.preact, i)));
+            e = output_err1<T>(a, to_f32(ldv<T>(a.out, i)), to_f32(ldv<T>(a.target, i)), to_f32(ldv<T>(a.preact, i)));
         }
         const float pcv = a.norm ? to_f32(ldv<T>(a.norm_in, i)) : 0.0f;
         const float rstd = (a.norm == 1 || a.norm == 2) ? to_f32(ldv<T>(a.norm_rstd, row)) : col.rstd[q];
@@ -885,11 +885,11 @@ __device__ __forceinline__ void err_row_ua(const ErrArgs &a, uint32_t row, uint3
     f32x4 e;
     if constexpr (FROM_SUM) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) e[j] = mk[j] * activation_derivative(a.act, s[j], pd[j], pa[j], a.leaky);
+        for (int j = 0; j < 4; ++j) e[j] = mk[j] * activation_derivative<T>(a.act, s[j], pd[j], pa[j], a.leaky);
     } else {
         const f32x4 out = G::ld(a.out, idx, cnt), tg = G::ld(a.target, idx, cnt), pre = G::ld(a.preact, idx, cnt);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) e[j] = output_err1(a, out[j], tg[j], pre[j]);
+        for (int j = 0; j < 4; ++j) e[j] = output_err1<T>(a, out[j], tg[j], pre[j]);
     }
     G::stf(a.grad, idx, e, cnt);
     f32x4 dp, dnw, dnb;

@@ -58,7 +58,7 @@ template <typename T> struct EpiFwdK {
         const f32x4 zt = round4<T>(z);
         f32x4 a;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) a[j] = activation(e.act, zt[j], e.leaky);
+        for (int j = 0; j < 4; ++j) a[j] = activation<T>(e.act, zt[j], e.leaky);
         store4_nt<T>(e.predrop, idx, a);
         if (e.use_dropout) {
             const float scale = 1.0f / (1.0f - e.p);
@@ -103,8 +103,8 @@ template <typename T> struct EpiFwdK {
         f32x4 a0, a1;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            a0[j] = activation(e.act, t0[j], e.leaky);
-            a1[j] = activation(e.act, t1[j], e.leaky);
+            a0[j] = activation<T>(e.act, t0[j], e.leaky);
+            a1[j] = activation<T>(e.act, t1[j], e.leaky);
         }
         st8(e.predrop, idx, a0, a1);
         if (e.use_dropout) {
@@ -138,7 +138,7 @@ template <typename T> struct EpiFwdK {
         const uint64_t idx = (uint64_t)m * e.ldc + n;
         st_t<T>(e.z_out, idx, zt);
         if (!e.fuse_act) return;
-        const float a = activation(e.act, to_f32(zt), e.leaky);
+        const float a = activation<T>(e.act, to_f32(zt), e.leaky);
         st_t<T>(e.predrop, idx, from_f32<T>(a));
         if (e.use_dropout) {
             if (dropout_u(n, m, e.seed + m * 7u) >= e.p) {
@@ -170,7 +170,7 @@ template <typename T> struct EpiFwdK {
             const uint64_t idx = (uint64_t)m * e.ldc + c;
             st_t<T>(e.z_out, idx, zt);
             if (e.fuse_act) {
-                const float a = activation(e.act, to_f32(zt), e.leaky);
+                const float a = activation<T>(e.act, to_f32(zt), e.leaky);
                 st_t<T>(e.predrop, idx, from_f32<T>(a));
                 if (e.use_dropout) {
                     if (dropout_u(c, m, e.seed + m * 7u) >= e.p) {
@@ -343,7 +343,7 @@ template <typename T> struct EpiErrK {
         f32x4 g, dp, dnw = {0, 0, 0, 0}, dnb = {0, 0, 0, 0};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            g[j] = (float)q.mk[j] * activation_derivative(e.act, v[j], (float)q.pd[j], (float)q.pa[j], e.leaky);
+            g[j] = (float)q.mk[j] * activation_derivative<T>(e.act, v[j], (float)q.pd[j], (float)q.pa[j], e.leaky);
             dp[j] = g[j];
             if (e.norm) {
                 const float p = (float)q.pn[j];

@@ -147,13 +147,37 @@ __host__ __device__ __forceinline__ bool act_uses_output(uint32_t act) { return 
 __host__ __device__ __forceinline__ bool act_uses_input(uint32_t act) { return act == 6 || act == 7; }
 
 // math.cuh:45-53.  The 64-bit product col * 6364136223846793005 keeps only its
-// low 32 bits in the 32-bit state, i.e. col * 0x4C957F2D mod 2^32.
-__device__ __forceinline__ float dropout_u(uint32_t col, uint32_t row, uint32_t seed) {
-    uint32_t s = (row * 1103515245u) ^ (col * 0x4C957F2Du) ^ seed;
+// low 32 bits in the 32-bit state, i.e. col * 0x4C957F2D mod 2^32.  The state
+// is (row * 1103515245) ^ (col * 0x4C957F2D) ^ seed: dropout_bits takes the
+// column product and the row key (row * 1103515245) ^ seed separately, so a
+// thread walking consecutive columns adds the constant instead of multiplying.
+constexpr uint32_t kDropColMul = 0x4C957F2Du;
+__host__ __device__ __forceinline__ uint32_t dropout_rowkey(uint32_t row, uint32_t seed) {
+    return (row * 1103515245u) ^ seed;
+}
+__host__ __device__ __forceinline__ uint32_t dropout_bits(uint32_t colmul, uint32_t rowkey) {
+    uint32_t s = rowkey ^ colmul;
     s = s ^ (s >> 17);
     s = s * 1103515245u + 12345u;
-    s = s ^ (s >> 15);
-    return (float)s / 4294967296.0f;
+    return s ^ (s >> 15);
+}
+__device__ __forceinline__ float dropout_u(uint32_t col, uint32_t row, uint32_t seed) {
+    return (float)dropout_bits(col * kDropColMul, dropout_rowkey(row, seed)) / 4294967296.0f;
+}
+// The keep test dropout_u(...) >= p as an integer compare, bits >= keep_min:
+// (float)s is monotone in s, so {s : (float)s / 2^32 >= p} is [keep_min, 2^32)
+// (keep_min = 2^32: never, e.g. p NaN).  Host-side, by bisection with the same
+// round-to-nearest-even u32 -> f32 conversion the device's v_cvt_f32_u32 does.
+inline uint64_t dropout_keep_min(float p) {
+    uint64_t lo = 0, hi = 1ull << 32;   // answer in [lo, hi]
+    while (lo < hi) {
+        const uint64_t mid = lo + (hi - lo) / 2;
+        if ((float)(uint32_t)mid / 4294967296.0f >= p)
+            hi = mid;
+        else
+            lo = mid + 1;
+    }
+    return lo;
 }
 
 // util.cu:175-215 — element-local norm gradient.

@@ -163,6 +163,82 @@ template <typename T> __device__ __forceinline__ void nt_store(void *p, uint64_t
     __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t *>(reinterpret_cast<T *>(p) + idx));
 }
 
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef float f2_t __attribute__((ext_vector_type(2)));
+// Two fp16 values <-> their 32-bit word.  The word is a by-value parameter:
+// __builtin_bit_cast applied directly to a vector element (w[q]) reads element 0
+// whatever q is (seen with this compiler), so it never takes one.
+__device__ __forceinline__ h2_t h2_of(uint32_t w) { return __builtin_bit_cast(h2_t, w); }
+__device__ __forceinline__ uint32_t word_of(h2_t h) { return __builtin_bit_cast(uint32_t, h); }
+
+// One 8-element chunk of an fp16 row (norm_rows_reg_kernel, 16-byte aligned rows)
+// from the raw prenorm bits zr and their fp32 values z: RMSNorm's fp16
+// products on packed pairs (v_pk_mul_f16), conversions back to fp16 two at a
+// time (v_cvt_pk_f16_f32), the centered cache of RMSNorm stored from the raw
+// bits, and the dropout keep test as an integer compare on hash bits whose
+// column product advances by a constant.  Per element the same values as the
+// general path below.
+__device__ __forceinline__ void norm_chunk_h(const RowNormArgs &a, uint64_t idx, uint32_t row, uint32_t c0,
+                                             u32x4_t zr, const float *z, float mean, float rstd32, half_t rstd_t,
+                                             float scale) {
+    const u32x4_t gr = *reinterpret_cast<const u32x4_t *>(reinterpret_cast<const half_t *>(a.norm_w) + c0);
+    u32x4_t pre, cen;
+    if (a.norm == 1) {
+        // (prenorm * rstd) * norm_w in fp16 (forward.cu:61-72): the product of two fp16
+        // values is exact in fp32, so rounding it to fp16 is one fp16 multiply
+        const h2_t r2 = {rstd_t, rstd_t};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) pre[q] = word_of((h2_of(zr[q]) * r2) * h2_of(gr[q]));
+        cen = zr;   // RMSNorm's centered cache is prenorm itself
+    } else {
+        const u32x4_t br = *reinterpret_cast<const u32x4_t *>(reinterpret_cast<const half_t *>(a.norm_b) + c0);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const f2_t v = {z[2 * q] - mean, z[2 * q + 1] - mean};
+            const f2_t g = __builtin_convertvector(h2_of(gr[q]), f2_t);
+            const f2_t b = __builtin_convertvector(h2_of(br[q]), f2_t);
+            cen[q] = word_of(__builtin_convertvector(v, h2_t));
+            const f2_t pf = {fmaf(v.x * rstd32, g.x, b.x), fmaf(v.y * rstd32, g.y, b.y)};
+            pre[q] = word_of(__builtin_convertvector(pf, h2_t));
+        }
+    }
+    f2_t act[4];
+    u32x4_t pd;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const f2_t pf = __builtin_convertvector(h2_of(pre[q]), f2_t);
+        act[q] = f2_t{activation<half_t>(a.act, pf.x, a.leaky), activation<half_t>(a.act, pf.y, a.leaky)};
+        pd[q] = word_of(__builtin_convertvector(act[q], h2_t));
+    }
+    // nontemporal: five write streams, read again only by later kernels
+    nt_store<half_t>(a.centered, idx, cen);
+    nt_store<half_t>(a.preact, idx, pre);
+    nt_store<half_t>(a.predrop, idx, pd);
+    if (!a.use_dropout) {
+        nt_store<half_t>(a.out, idx, pd);
+        return;
+    }
+    const uint32_t rk = dropout_rowkey(row, a.seed + row * 7u);
+    const uint32_t cm0 = c0 * kDropColMul;
+    const half_t sc = (half_t)scale;
+    u32x4_t mk, ot;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const h2_t os = __builtin_convertvector(act[q] * scale, h2_t);
+        h2_t m2, o2;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const bool keep = (uint64_t)dropout_bits(cm0 + (uint32_t)(2 * q + h) * kDropColMul, rk) >= a.keep_min;
+            m2[h] = keep ? sc : (half_t)0;
+            o2[h] = keep ? os[h] : (half_t)0;
+        }
+        mk[q] = word_of(m2);
+        ot[q] = word_of(o2);
+    }
+    nt_store<half_t>(a.mask, idx, mk);
+    nt_store<half_t>(a.out, idx, ot);
+}
+
 // The same with the row held in registers: each element of prenorm is read
 // once, and every cache write is a 16-byte store when rows are 16-byte aligned
 // (VEC: a thread owns chunks of VW consecutive elements, chunk t + 256 i) or
@@ -178,6 +254,7 @@ template <typename T, bool VEC, int PER> __global__ void __launch_bounds__(256) 
     const T *pz = reinterpret_cast<const T *>(a.prenorm) + base;
     float z[E];
     bool in[PER];
+    u32x4_t zr[PER];   // raw chunks (the fp16 chunk path stores RMSNorm's centered cache from them)
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
         const uint32_t c0 = (threadIdx.x + 256u * i) * VW;
@@ -190,6 +267,7 @@ template <typename T, bool VEC, int PER> __global__ void __launch_bounds__(256) 
 #pragma unroll
                 for (int e = 0; e < VW; ++e) v[e] = (T)0;
             }
+            zr[i] = *reinterpret_cast<const u32x4_t *>(v);
 #pragma unroll
             for (int e = 0; e < VW; ++e) z[i * VW + e] = to_f32(v[e]);
         } else {
@@ -228,6 +306,10 @@ template <typename T, bool VEC, int PER> __global__ void __launch_bounds__(256) 
     for (int i = 0; i < PER; ++i) {
         if (!in[i]) continue;
         const uint32_t c0 = (threadIdx.x + 256u * i) * VW;
+        if constexpr (VEC && sizeof(T) == 2) {
+            norm_chunk_h(a, base + c0, row, c0, zr[i], &z[i * VW], mean, rstd32, rstd_t, scale);
+            continue;
+        }
         T cen[VW], pre[VW], pd[VW], mk[VW], ot[VW], g[VW], bb[VW];
         if constexpr (VEC) {
             *reinterpret_cast<u32x4_t *>(g) = *reinterpret_cast<const u32x4_t *>(reinterpret_cast<const T *>(a.norm_w) + c0);
@@ -476,8 +558,10 @@ template <typename T> static void launch_norm_rows(const RowNormArgs &a, hipStre
         hipLaunchKernelGGL(norm_rows_kernel<T>, g, b, 0, s, a);
 }
 
-hipError_t launch_norm_act(const RowNormArgs &a, hipStream_t s) {
-    if (a.m == 0 || a.n == 0) return hipSuccess;
+hipError_t launch_norm_act(const RowNormArgs &a0, hipStream_t s) {
+    if (a0.m == 0 || a0.n == 0) return hipSuccess;
+    RowNormArgs a = a0;
+    a.keep_min = dropout_keep_min(a.p);
     if (a.norm == 3) {
         if (a.dtype == 1)
             hipLaunchKernelGGL(norm_cols_kernel<half_t>, dim3(cdiv(a.n, 256)), dim3(256), 0, s, a);

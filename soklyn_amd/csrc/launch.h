@@ -119,6 +119,7 @@ struct RowNormArgs {
     float leaky, p;
     const void *prenorm, *norm_w, *norm_b;
     void *centered, *preact, *predrop, *out, *mask, *norm_rstd;
+    uint64_t keep_min;   // set by launch_norm_act: dropout_keep_min(p)
 };
 // fwd1 + fwd2 fused (RMS / LN per row; BN per column then act).
 hipError_t launch_norm_act(const RowNormArgs &a, hipStream_t s);

@@ -298,6 +298,17 @@ template <class E> struct EpiSums<E, std::void_t<decltype(E::kColSums)>> {
 template <class E, class = void> struct EpiVec8 { static constexpr bool value = false; };
 template <class E> struct EpiVec8<E, std::void_t<decltype(E::kVec)>> { static constexpr bool value = E::kVec == 8; };
 
+// MFMAs per DMA instruction in a tile's last k-step, where the refill of the
+// stage just read is issued (16x16x32 schedule): 1 = all of them behind the
+// first MFMAs.  Measured on C3 / C4 (steady clocks): every second MFMA runs the
+// forward 0.2357 -> 0.2317 ms and the fused hidden error 0.2689 -> 0.2672 ms,
+// while the fp32-store dX is fastest front-loaded (0.2178 ms; 0.2188 at 2,
+// 0.2224 at 4), so an epilogue may set its own kDmaSpacing.
+template <class E, class = void> struct EpiDmaSpacing { static constexpr int value = 2; };
+template <class E> struct EpiDmaSpacing<E, std::void_t<decltype(E::kDmaSpacing)>> {
+    static constexpr int value = E::kDmaSpacing;
+};
+
 template <bool KC, int NW, int NF, int MI, int R> struct DmaOpSel { typedef OpK<NW, NF, MI, R> type; };
 template <int NW, int NF, int MI, int R> struct DmaOpSel<false, NW, NF, MI, R> { typedef OpN<NW, NF, MI, R> type; };
 
@@ -421,6 +432,8 @@ __global__ void __launch_bounds__(64 * NW)
         // still be pending: the other A fragments of its k-step plus, from row 1
         // on, this k-step's B reads (capped at the counter's 15: stricter).
         typename OA::Frag &fa1 = fa[0];
+        constexpr int SPC = EpiDmaSpacing<Epi>::value;
+        static_assert(NDMA * SPC <= C::MT * C::NTL, "every DMA instruction follows an MFMA of the last k-step");
         constexpr int W0 = (C::MT - 1) * OA::RPF < 15 ? (C::MT - 1) * OA::RPF : 15;
         constexpr int W1 = (C::MT - 1) * OA::RPF + C::NTL * OB::RPF < 15
                                ? (C::MT - 1) * OA::RPF + C::NTL * OB::RPF : 15;
@@ -479,7 +492,7 @@ __global__ void __launch_bounds__(64 * NW)
                     for (int j = 0; j < C::NTL; ++j) {
                         mfma1(1, i, j);
                         const int q = i * C::NTL + j;
-                        if (q < NDMA) dma(kn, s, q);
+                        if (q % SPC == 0 && q / SPC < NDMA) dma(kn, s, q / SPC);
                         if (i == 0) ob.read_frag(fb[0], (s ^ 1) * C::STAGEB, 0, j);
                         __builtin_amdgcn_sched_barrier(0);
                     }

@@ -328,8 +328,10 @@ template <typename T> struct EpiErrK {
         c.rstd = e.norm == 3 ? load4<T>(e.norm_rstd, n) : f32x4{0, 0, 0, 0};
         return c;
     }
+    // nontemporal: the forward caches are read once here (C4's fused hidden error
+    // 0.268 -> 0.262 ms against plain loads)
     __device__ __forceinline__ static f16x4 ld4h(const void *p, uint64_t idx) {
-        return *reinterpret_cast<const f16x4 *>(reinterpret_cast<const half_t *>(p) + idx);
+        return __builtin_nontemporal_load(reinterpret_cast<const f16x4 *>(reinterpret_cast<const half_t *>(p) + idx));
     }
     __device__ __forceinline__ static void load(const ErrEpi &e, uint64_t idx, uint32_t m, Pre &q) {
         static_assert(sizeof(T) == 2, "the 256x256 kernel is fp16");

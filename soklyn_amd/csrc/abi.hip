@@ -322,7 +322,8 @@ hipError_t timed_gemm(skl_ctx *ctx, const GemmLaunch &g0, GemmKind kind, float *
 // buffer has room for the padded grid (p.Mp x p.Np at its ldc), so the kernel
 // may write all of it (rows and columns past M, N come out zero).
 // vec (a dW only): the bias / norm-parameter update to run inside the split-K
-// reduction's launch when there is one; *vec_done says whether it ran.
+// reduction's launch or the fused direct-to-LDS kernel when there is one;
+// *vec_done says whether it ran.
 int32_t exec_gemm(skl_ctx *ctx, GemmLaunch g, const GemmPlan &p, char *ws, bool full_out = false,
                   const VecOptArgs *vec = nullptr, bool *vec_done = nullptr) {
     if (vec_done) *vec_done = false;
@@ -369,6 +370,13 @@ int32_t exec_gemm(skl_ctx *ctx, GemmLaunch g, const GemmPlan &p, char *ws, bool 
         g.mv = full_out ? p.Mp : M;
         g.nv = full_out ? p.Np : N;
         g.tile = p.tile;
+        if (vec && g.op == Op::DwOpt && p.splits == 1) {
+            // the bias / norm-parameter update rides in the fused kernel's launch
+            g.opt.vec = *vec;
+            g.opt.vec.cpb = vec_opt_cpb(vec->splits);
+            g.opt.vec_blocks = (vec->n + g.opt.vec.cpb - 1) / g.opt.vec.cpb;
+            if (vec_done) *vec_done = true;
+        }
         g.M = p.Mp;
         g.N = p.Np;
         g.K = p.Kp;

@@ -231,6 +231,7 @@ struct EpiStoreK {
 // ---- dW + optimiser on W (fused) -----------------------------------------------
 template <typename T> struct EpiOptK {
     typedef OptEpi Params;
+    typedef T elem;
     __device__ __forceinline__ static uint32_t ldc(const OptEpi &e) { return e.ldc; }
     __device__ __forceinline__ static OptEpi at_split(const OptEpi &e, uint32_t) { return e; }
     struct Col {};

@@ -60,6 +60,7 @@
 #include <type_traits>
 
 #include "gemm.h"
+#include "vec_opt.h"
 
 namespace skl {
 
@@ -667,6 +668,14 @@ __global__ void __launch_bounds__(64 * NW)
         static_assert(NW * RPS * 3 * C::BN * 4 <= EPI_BYTES, "column-sum staging fits the epilogue's LDS");
         lds_barrier();   // every wave is done reading E
         Epi::template flush<NW, C::BN>(eps, csum, E, tid, tm, n0);
+    }
+    // The fused dW + optimiser form also runs the bias / norm-parameter update
+    // (independent of W): workgroup w takes its blocks w, w + grid, ... after
+    // its tile, which saves that update a launch of its own (its own LDS).
+    if constexpr (std::is_same<typename Epi::Params, OptEpi>::value) {
+        const uint32_t nwg = gridDim.x * gridDim.y;
+        for (uint32_t blk = blockIdx.x + gridDim.x * blockIdx.y; blk < ep.vec_blocks; blk += nwg)
+            vec_opt_block<typename Epi::elem, 64 * NW>(ep.vec, blk);
     }
 }
 

@@ -22,6 +22,20 @@ struct FwdEpi {
     uint32_t ldc, pad;
 };
 
+// The bias / norm-parameter update: column partial sums -> optimiser step.
+struct VecOptArgs {
+    uint32_t dtype, rows, n, splits;
+    const float *src[3];          // d_prenorm (bias), d_norm_w, d_norm_b (null = skip)
+    float *partials;              // [splits][3][n]
+    // targets: 0 bias, 1 norm_w, 2 norm_b
+    void *param[3];
+    float *master[3], *dv[3], *dm[3];
+    uint32_t enabled[3];
+    OptParams opt[3];
+    float lr, clamp, inv_m;
+    uint32_t cpb;                 // columns per workgroup (set by the launchers)
+};
+
 // dW + optimiser on W (backward.cu:180-186 + 227-233).
 struct OptEpi {
     float *master;        // fp32 master (the parameter itself for fp32 blocks)
@@ -30,6 +44,10 @@ struct OptEpi {
     OptParams opt;
     float lr, clamp, inv_m, regu_coeff;
     uint32_t regularisation, ldc;
+    // the 256x256 kernel's fused form only: after its tiles, workgroup w runs
+    // blocks w, w + grid, ... < vec_blocks of the bias / norm-parameter update
+    uint32_t vec_blocks;
+    VecOptArgs vec;
 };
 
 // Plain fp32 store (input gradient) or split-K partial store.
@@ -160,18 +178,6 @@ hipError_t launch_error_skinny(const ErrArgs &a, float *partials, uint32_t split
 
 // Column sums of up to three fp32 [rows x n] arrays into partials
 // [splits x 3 x n]; then the bias / norm-parameter optimiser.
-struct VecOptArgs {
-    uint32_t dtype, rows, n, splits;
-    const float *src[3];          // d_prenorm (bias), d_norm_w, d_norm_b (null = skip)
-    float *partials;              // [splits][3][n]
-    // targets: 0 bias, 1 norm_w, 2 norm_b
-    void *param[3];
-    float *master[3], *dv[3], *dm[3];
-    uint32_t enabled[3];
-    OptParams opt[3];
-    float lr, clamp, inv_m;
-    uint32_t cpb;                 // columns per workgroup (set by the launchers)
-};
 hipError_t launch_colsum(const VecOptArgs &a, hipStream_t s);
 // Columns per workgroup of the parameter update for `splits` partial rows.
 uint32_t vec_opt_cpb(uint32_t splits);

@@ -192,6 +192,7 @@ template <typename T> struct EpiFwdK {
 // ---- plain fp32 store (input gradient; split-K partials) -----------------------
 struct EpiStoreK {
     static constexpr int kDmaSpacing = 1;   // front-loaded refill (measured fastest for dX)
+    static constexpr int kReadsPerMfma = 1; // 32x32 schedule (the split-K dW partial)
     typedef StoreEpi Params;
     __device__ __forceinline__ static uint32_t ldc(const StoreEpi &e) { return e.ldc; }
     // the partial plane of split-K slice `split`

@@ -310,6 +310,14 @@ template <class E> struct EpiDmaSpacing<E, std::void_t<decltype(E::kDmaSpacing)>
     static constexpr int value = E::kDmaSpacing;
 };
 
+// 32x32x16 schedule: the next k-step's fragment reads issued behind each MFMA
+// (2 at 8 waves).  The split-K dW partial (fp32 store) runs faster with 1 (C4
+// step 2.578 -> 2.568 ms), dW + Adam slower (0.2825 -> 0.288 ms).
+template <class E, int NW, class = void> struct EpiReadsPerMfma { static constexpr int value = NW == 8 ? 2 : 1; };
+template <class E, int NW> struct EpiReadsPerMfma<E, NW, std::void_t<decltype(E::kReadsPerMfma)>> {
+    static constexpr int value = E::kReadsPerMfma;
+};
+
 template <bool KC, int NW, int NF, int MI, int R> struct DmaOpSel { typedef OpK<NW, NF, MI, R> type; };
 template <int NW, int NF, int MI, int R> struct DmaOpSel<false, NW, NF, MI, R> { typedef OpN<NW, NF, MI, R> type; };
 
@@ -377,7 +385,7 @@ __global__ void __launch_bounds__(64 * NW)
     constexpr int NFR = C::MT + C::NTL;            // fragments per set
     constexpr int NMM = C::MT * C::NTL;            // MFMAs per k-step
     constexpr int NDMA = OA::IPO + OB::IPO;        // DMA instructions per tile and wave
-    constexpr int FPM = NW == 8 ? 2 : 1;           // fragment reads behind each MFMA
+    constexpr int FPM = EpiReadsPerMfma<Epi, NW>::value;   // fragment reads behind each MFMA
     static_assert(NFR <= NMM * FPM && NDMA <= NMM, "every read and DMA has an MFMA to follow");
     auto read_frag = [&](int set, int stage, int ks, int f) {
         if (f < C::MT)

@@ -681,6 +681,16 @@ struct ErrAcc {   // running column sums of a thread's 4 elements
 // for fp16 blocks); the n >= 4 it needs puts a chunk's elements in at most two
 // rows, and both rows' sums are formed before the element picks its own.
 constexpr int ERR_UB = 4;
+// 4 consecutive T elements with the nontemporal hint (read once).
+template <typename T> __device__ __forceinline__ f32x4 load4_nt(const void *p, uint64_t i) {
+    if constexpr (sizeof(T) == 2) {
+        const f16x4 h =
+            __builtin_nontemporal_load(reinterpret_cast<const f16x4 *>(reinterpret_cast<const half_t *>(p) + i));
+        return f32x4{(float)h.x, (float)h.y, (float)h.z, (float)h.w};
+    } else {
+        return __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(reinterpret_cast<const float *>(p) + i));
+    }
+}
 struct FlatPos {
     uint32_t r[4], c[4];
 };
@@ -722,6 +732,12 @@ template <typename T, int SRC, int B, bool NORM, int UB>
 __device__ __forceinline__ void err_flat_bands(const ErrArgs &a, uint32_t b, uint32_t j, uint32_t s_ld,
                                                const FlatPos &fp, const ErrCol<T> &col, ErrAcc &acc) {
     const uint32_t n = a.n;
+    // fp16 blocks without a norm (the single-block error from a sum, C3) read the
+    // per-element operands with the nontemporal hint: the C3 error call 0.139 ->
+    // 0.118 ms, the step +1.4%; with a norm (C4, C5) it changed nothing or cost
+    // up to 0.5%, and C2's fp32 call (its 50 MB stay in the last-level cache)
+    // 0.0176 -> 0.019 ms.  Stores stay plain (nontemporal ones cost 10-15% here).
+    constexpr bool NTL = !NORM && sizeof(T) == 2;
     f32x4 x[3][UB], mk[UB], pc[UB], rs[UB];
     SkRows<T, B> ar[SRC == 2 ? UB : 1];
 #pragma unroll
@@ -729,18 +745,24 @@ __device__ __forceinline__ void err_flat_bands(const ErrArgs &a, uint32_t b, uin
         const uint32_t row0 = (b + u) * B;
         const uint64_t base = (uint64_t)row0 * n + 4ull * j;
         if constexpr (SRC == 1) {
-            // (one 16-byte load when B == 1: the four addresses are consecutive)
+            if constexpr (B == 1 && NTL) {
+                // the four addresses are consecutive and 16-byte aligned (the launcher
+                // checks s_ld % 4 == 0)
+                x[0][u] = load4_nt<float>(a.s, (uint64_t)row0 * s_ld + fp.c[0]);
+            } else {
+                // (one 16-byte load when B == 1: the four addresses are consecutive)
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-                x[0][u][q] = a.s[(uint64_t)(row0 + fp.r[q]) * s_ld + fp.c[q]];
+                for (int q = 0; q < 4; ++q)
+                    x[0][u][q] = a.s[(uint64_t)(row0 + fp.r[q]) * s_ld + fp.c[q]];
+            }
         } else if constexpr (SRC == 2) {
             load16<T>(ar[u].lo, a.sk_a, row0 + fp.r[0]);
             if constexpr (B > 1) load16<T>(ar[u].hi, a.sk_a, row0 + fp.r[3]);
         }
         if constexpr (SRC != 0) {
-            x[1][u] = load4<T>(a.predrop, base);
-            x[2][u] = load4<T>(a.preact, base);
-            mk[u] = load4<T>(a.mask, base);
+            x[1][u] = NTL ? load4_nt<T>(a.predrop, base) : load4<T>(a.predrop, base);
+            x[2][u] = NTL ? load4_nt<T>(a.preact, base) : load4<T>(a.preact, base);
+            mk[u] = NTL ? load4_nt<T>(a.mask, base) : load4<T>(a.mask, base);
         } else {
             x[0][u] = load4<T>(a.out, base);
             x[1][u] = load4<T>(a.target, base);
@@ -1117,7 +1139,10 @@ template <bool FROM_SUM, typename T>
 static hipError_t launch_error_t(const ErrArgs &a0, float *partials, uint32_t splits, hipStream_t s) {
     ErrArgs a = a0;
     a.norm_in = a.norm == 1 ? a.prenorm : a.centered;
-    if (!err_aligned(a, FROM_SUM, partials)) {
+    // the flat kernel reads a row of s as 16-byte chunks when n % 4 == 0: the
+    // pitch must keep them aligned
+    const bool s_ok = !FROM_SUM || (a.n & 3u) != 0 || ((a.s_ld ? a.s_ld : a.n) & 3u) == 0;
+    if (!s_ok || !err_aligned(a, FROM_SUM, partials)) {
         hipLaunchKernelGGL((error_cols_kernel<T, FROM_SUM>), dim3(cdiv(a.n, 1024), splits), dim3(256), 0, s, a,
                            partials, cdiv(a.rows, splits));
         return hipGetLastError();

@@ -310,10 +310,11 @@ class MlpBench:
         self.step_no = 0
         self.flops = mlp_flops(dims, M)
         # the roofline kernel: the GEMM of the hidden error of layer `timed_layer`, dX
-        # through the weights of the layer above it (the call also runs the error kernel)
+        # through the weights of the layer above it (the call also runs the error
+        # kernel, then the layer's dW and optimiser step)
         k = cfg["timed_layer"]
         self.timed = f"hidden_error_gemm_layer{k}"
-        self.calls = (f"hidden_error_layer{k}",)
+        self.calls = (f"backward_hidden_layer{k}",)
         self.gemms = (self.timed,)
         self.kernel_flops = {self.timed: 2.0 * M * dims[k + 1] * dims[k + 2]}
         self.hbm_bytes = {}
@@ -334,10 +335,10 @@ class MlpBench:
                 self.ctx.time_next_gemm(*gev[0])
             if timed and ev is not None:
                 ev[0][0].record(self.stream)
-            b[i].hidden_error(b[i + 1], M)
+            # gpu_hidden_layer_backward_pass (ffn.rs:156 -> mlp.rs:728): hidden error, then dW
+            b[i].backward_hidden(b[i + 1], b[i - 1].out if i > 0 else self.x, self.tc, self.step_no)
             if timed and ev is not None:
                 ev[0][1].record(self.stream)
-            b[i].backward(b[i - 1].out if i > 0 else self.x, self.tc, self.step_no)
 
 
 def main():

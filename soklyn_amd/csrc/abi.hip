@@ -6,6 +6,7 @@
 // the MI355X kernels on the context's stream.
 #include <float.h>
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <cmath>
@@ -31,6 +32,25 @@ struct ColSums {
     bool valid;
 };
 
+// A block's fp16 d_prenorm copied zero-padded to [round_up(rows, 256) x ld],
+// ld = round_up(n, 256), by the GEMM that first needed it padded (a dW reads
+// d_prenorm_h as its B, the hidden error of the layer below and the input
+// gradient as their A; the direct-to-LDS kernel cannot read an odd-width or
+// ragged operand in place).  The context keeps it so that the other GEMM on the
+// same d_prenorm_h reads it instead of padding it again: when it mirrors the
+// same buffer, rows and n and was made by the same call or the one just before
+// it (as with ColSums), and no error entry point has rewritten d_prenorm_h since.
+// One slot per block, up to kPadSlots (the least recently made one reused).
+constexpr int kPadSlots = 8;
+struct PadCopy {
+    half_t *buf;
+    size_t bytes;
+    const void *src;   // the d_prenorm_h it mirrors
+    uint32_t rows, n, ld;
+    uint64_t call;
+    bool valid;
+};
+
 struct skl_ctx {
     int device;
     uint32_t tile_dim;
@@ -43,6 +63,8 @@ struct skl_ctx {
     float *cols;         // ColSums storage
     size_t cols_bytes;
     ColSums cs;
+    PadCopy pads[kPadSlots];
+    bool keep_pads;      // SOKLYN_PAD_KEEP=0 at skl_ctx_create: GEMMs pad d_prenorm_h into the workspace every time
     hipEvent_t gemm_start, gemm_stop;   // skl_ctx_time_next_gemm
     void *scratch;       // device address of this device's copy of `scratch` (below)
 };
@@ -157,6 +179,61 @@ bool cols_match(const skl_ctx *ctx, const skl_dense_desc *b, uint32_t rows) {
            c.norm == b->norm && (b->norm == SKL_NORM_DISABLED || (c.dnw == b->d_norm_w && c.dnb == b->d_norm_b));
 }
 
+uint32_t round_up(uint32_t v, uint32_t m) { return (v + m - 1) / m * m; }
+
+// An error entry point rewrote d_prenorm_h: its padded copy is stale.
+void pad_forget(skl_ctx *ctx, const void *src) {
+    for (PadCopy &c : ctx->pads)
+        if (c.src == src) c.valid = false;
+}
+
+// The current padded copy of a GEMM operand stored as [rows x cols] at pitch ld, if any.
+const PadCopy *pad_copy_of(const skl_ctx *ctx, const void *p, uint32_t rows, uint32_t cols, uint32_t ld) {
+    for (const PadCopy &c : ctx->pads)
+        if (c.valid && c.src == p && c.rows == rows && c.n == cols && ld == cols && c.call + 1 >= ctx->calls)
+            return &c;
+    return nullptr;
+}
+
+// Pads d_prenorm_h p ([rows x cols] at pitch ld) into its slot (the one already
+// mirroring p, else the least recently made) and records it; *out = nullptr
+// when the copy would not suit the kernel's 32-bit operand offsets.
+int32_t pad_keep(skl_ctx *ctx, const void *p, uint32_t rows, uint32_t cols, uint32_t ld, const PadCopy **out) {
+    *out = nullptr;
+    const uint32_t rows_p = round_up(rows, 256), ld_p = round_up(cols, 256);
+    const size_t need = (size_t)rows_p * ld_p * sizeof(half_t);
+    if (need >= (size_t(1) << 32)) return SKL_OK;
+    PadCopy *c = &ctx->pads[0];
+    for (PadCopy &s : ctx->pads) {
+        if (s.src == p) {
+            c = &s;
+            break;
+        }
+        if (s.call < c->call) c = &s;
+    }
+    c->valid = false;
+    if (need > c->bytes) {
+        SKL_TRY(hipStreamSynchronize(ctx->stream));
+        if (c->buf) SKL_TRY(hipFree(c->buf));
+        c->buf = nullptr;
+        c->bytes = 0;
+        void *b = nullptr;
+        SKL_TRY(hipMalloc(&b, need));
+        c->buf = reinterpret_cast<half_t *>(b);
+        c->bytes = need;
+    }
+    // every element of [rows_p x ld_p]: the source, then zeros
+    SKL_TRY(launch_pad_h(p, rows, cols, ld, c->buf, rows_p, ld_p, ctx->stream));
+    c->src = p;
+    c->rows = rows;
+    c->n = cols;
+    c->ld = ld_p;
+    c->call = ctx->calls;
+    c->valid = true;
+    *out = c;
+    return SKL_OK;
+}
+
 size_t elem_size(uint32_t dtype) { return dtype == SKL_F16 ? 2 : 4; }
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -182,8 +259,6 @@ struct GemmPlan {
     size_t a_bytes, b_bytes, part_bytes;
     size_t bytes() const { return a_bytes + b_bytes + part_bytes; }
 };
-
-uint32_t round_up(uint32_t v, uint32_t m) { return (v + m - 1) / m * m; }
 
 // A stored operand the DMA kernel can read in place: rows x cols (k-contiguous:
 // rows = m or n, cols = k; else rows = k, cols = m or n) with whole tiles.
@@ -323,9 +398,11 @@ hipError_t timed_gemm(skl_ctx *ctx, const GemmLaunch &g0, GemmKind kind, float *
 // may write all of it (rows and columns past M, N come out zero).
 // vec (a dW only): the bias / norm-parameter update to run inside the split-K
 // reduction's launch or the fused direct-to-LDS kernel when there is one;
-// *vec_done says whether it ran.
+// *vec_done says whether it ran.  keep: KEEP_A / KEEP_B, the operand is a
+// d_prenorm_h whose padded copy goes to the context's PadCopy slots.
+enum : uint32_t { KEEP_A = 1, KEEP_B = 2 };
 int32_t exec_gemm(skl_ctx *ctx, GemmLaunch g, const GemmPlan &p, char *ws, bool full_out = false,
-                  const VecOptArgs *vec = nullptr, bool *vec_done = nullptr) {
+                  const VecOptArgs *vec = nullptr, bool *vec_done = nullptr, uint32_t keep = 0) {
     if (vec_done) *vec_done = false;
     char *wa = ws, *wb = ws + p.a_bytes, *wpart = ws + p.a_bytes + p.b_bytes;
     const OptEpi oe = g.opt;
@@ -351,21 +428,45 @@ int32_t exec_gemm(skl_ctx *ctx, GemmLaunch g, const GemmPlan &p, char *ws, bool 
         return SKL_OK;
     }
     if (p.dma) {
+        // a d_prenorm_h padded by the GEMM before (or padded now into a kept slot),
+        // else a padded copy in the workspace
         if (p.pad_a) {
-            if (g.a_kcontig)
-                SKL_TRY(launch_pad_h(g.A, g.M, g.K, g.lda, wa, p.Mp, p.Kp, ctx->stream));
-            else
-                SKL_TRY(launch_pad_h(g.A, g.K, g.M, g.lda, wa, p.Kp, p.Mp, ctx->stream));
-            g.A = wa;
-            g.lda = g.a_kcontig ? p.Kp : p.Mp;
+            const uint32_t rows = g.a_kcontig ? g.M : g.K, cols = g.a_kcontig ? g.K : g.M;
+            const PadCopy *c = pad_copy_of(ctx, g.A, rows, cols, g.lda);
+            if (!c && (keep & KEEP_A) && ctx->keep_pads) {
+                const int32_t r = pad_keep(ctx, g.A, rows, cols, g.lda, &c);
+                if (r) return r;
+            }
+            if (c) {
+                g.A = c->buf;
+                g.lda = c->ld;
+            } else {
+                if (g.a_kcontig)
+                    SKL_TRY(launch_pad_h(g.A, g.M, g.K, g.lda, wa, p.Mp, p.Kp, ctx->stream));
+                else
+                    SKL_TRY(launch_pad_h(g.A, g.K, g.M, g.lda, wa, p.Kp, p.Mp, ctx->stream));
+                g.A = wa;
+                g.lda = g.a_kcontig ? p.Kp : p.Mp;
+            }
         }
         if (p.pad_b) {
-            if (g.b_kcontig)
-                SKL_TRY(launch_pad_h(g.B, g.N, g.K, g.ldb, wb, p.Np, p.Kp, ctx->stream));
-            else
-                SKL_TRY(launch_pad_h(g.B, g.K, g.N, g.ldb, wb, p.Kp, p.Np, ctx->stream));
-            g.B = wb;
-            g.ldb = g.b_kcontig ? p.Kp : p.Np;
+            const uint32_t rows = g.b_kcontig ? g.N : g.K, cols = g.b_kcontig ? g.K : g.N;
+            const PadCopy *c = pad_copy_of(ctx, g.B, rows, cols, g.ldb);
+            if (!c && (keep & KEEP_B) && ctx->keep_pads) {
+                const int32_t r = pad_keep(ctx, g.B, rows, cols, g.ldb, &c);
+                if (r) return r;
+            }
+            if (c) {
+                g.B = c->buf;
+                g.ldb = c->ld;
+            } else {
+                if (g.b_kcontig)
+                    SKL_TRY(launch_pad_h(g.B, g.N, g.K, g.ldb, wb, p.Np, p.Kp, ctx->stream));
+                else
+                    SKL_TRY(launch_pad_h(g.B, g.K, g.N, g.ldb, wb, p.Kp, p.Np, ctx->stream));
+                g.B = wb;
+                g.ldb = g.b_kcontig ? p.Kp : p.Np;
+            }
         }
         g.mv = full_out ? p.Mp : M;
         g.nv = full_out ? p.Np : N;
@@ -540,6 +641,11 @@ int32_t skl_ctx_create(int32_t ordinal, uint32_t tile_dim, skl_ctx **out) {
     c->ws = nullptr;
     c->ws_bytes = 0;
     {
+        // SOKLYN_PAD_KEEP=0: no kept padded copies (A/B comparisons)
+        const char *e = getenv("SOKLYN_PAD_KEEP");
+        c->keep_pads = !(e && atoi(e) == 0);
+    }
+    {
         const int32_t sr = scratch_address(ordinal, &c->scratch);
         if (sr != SKL_OK) {
             delete c;
@@ -563,6 +669,8 @@ int32_t skl_ctx_destroy(skl_ctx *ctx) {
     hipStreamSynchronize(ctx->stream);
     if (ctx->ws) hipFree(ctx->ws);
     if (ctx->cols) hipFree(ctx->cols);
+    for (PadCopy &c : ctx->pads)
+        if (c.buf) hipFree(c.buf);
     hipStreamDestroy(ctx->own_stream);
     delete ctx;
     return SKL_OK;
@@ -776,6 +884,7 @@ int32_t skl_dense_output_error(skl_ctx *ctx, const skl_dense_desc *b, const void
     a.d_prenorm_h = b->dtype == SKL_F16 ? reinterpret_cast<half_t *>(b->d_prenorm_h) : nullptr;
     uint32_t splits = 0;
     if ((r = ensure_cols(ctx, target_rows, b->outputs, &splits))) return r;
+    pad_forget(ctx, b->d_prenorm_h);
     SKL_TRY(launch_output_error(a, ctx->cols, splits, ctx->stream));
     record_cols(ctx, b, target_rows, splits);
     return finish(ctx);
@@ -828,6 +937,8 @@ static int32_t hidden_error_impl(skl_ctx *ctx, const skl_dense_desc *cur, const 
     a.d_norm_b = cur->d_norm_b;
     a.d_prenorm_h = cur->dtype == SKL_F16 ? reinterpret_cast<half_t *>(cur->d_prenorm_h) : nullptr;
     const void *next_dp = cur->dtype == SKL_F16 ? next->d_prenorm_h : next->d_prenorm;
+    const uint32_t keep = cur->dtype == SKL_F16 ? KEEP_A : 0;   // next_dp is a d_prenorm_h
+    pad_forget(ctx, cur->d_prenorm_h);
 
     // A next layer of at most 16 outputs: its GEMM would pad k to 128, so the
     // error kernel forms s = next.d_prenorm . next.W^T itself, per element, from
@@ -898,7 +1009,7 @@ static int32_t hidden_error_impl(skl_ctx *ctx, const skl_dense_desc *cur, const 
         if ((r = ensure_ws(ctx, plan.bytes()))) return r;
         e.partials = ctx->cols;
         g.op = Op::HiddenErr;
-        if ((r = exec_gemm(ctx, g, plan, reinterpret_cast<char *>(ctx->ws)))) return r;
+        if ((r = exec_gemm(ctx, g, plan, reinterpret_cast<char *>(ctx->ws), false, nullptr, nullptr, keep))) return r;
         record_cols(ctx, cur, batch, tiles_m);
         return SKL_OK;
     }
@@ -909,7 +1020,8 @@ static int32_t hidden_error_impl(skl_ctx *ctx, const skl_dense_desc *cur, const 
     float *sum = reinterpret_cast<float *>(ctx->ws);
     g.st.out = sum;
     g.st.ldc = s_ld;
-    if ((r = exec_gemm(ctx, g, plan, reinterpret_cast<char *>(ctx->ws) + s_bytes, true))) return r;
+    if ((r = exec_gemm(ctx, g, plan, reinterpret_cast<char *>(ctx->ws) + s_bytes, true, nullptr, nullptr, keep)))
+        return r;
 
     // ... then the error kernel on it
     a.s = sum;
@@ -1032,7 +1144,7 @@ static int32_t backward_impl(skl_ctx *ctx, const skl_dense_desc *b, const void *
     // parameter update then rides in the dW's split-K reduction launch when it has one
     if (any_vec && !cached) SKL_TRY(launch_colsum(v, ctx->stream));
     bool vec_done = false;
-    if ((r = exec_gemm(ctx, g, plan, ws, false, any_vec ? &v : nullptr, &vec_done))) return r;
+    if ((r = exec_gemm(ctx, g, plan, ws, false, any_vec ? &v : nullptr, &vec_done, f16 ? KEEP_B : 0))) return r;
     if (any_vec && !vec_done) SKL_TRY(launch_vec_opt(v, ctx->stream));
     return SKL_OK;
 }
@@ -1113,6 +1225,7 @@ int32_t skl_dense_error_from_sum(skl_ctx *ctx, const skl_dense_desc *b, const fl
     const ErrArgs a = error_from_sum_args(b, s, batch);
     uint32_t splits = 0;
     if ((r = ensure_cols(ctx, batch, b->outputs, &splits))) return r;
+    pad_forget(ctx, b->d_prenorm_h);
     SKL_TRY(launch_error_from_sum(a, ctx->cols, splits, ctx->stream));
     record_cols(ctx, b, batch, splits);
     return finish(ctx);
@@ -1128,6 +1241,7 @@ int32_t skl_dense_error_from_sum_noalloc(skl_ctx *ctx, const skl_dense_desc *b, 
     if ((r = zero_dnorm_tail(ctx, b, batch))) return r;
     const ErrArgs a = error_from_sum_args(b, s, batch);
     // every split writes all of its partial-sum rows: nothing in the scratch needs clearing
+    pad_forget(ctx, b->d_prenorm_h);
     SKL_TRY(launch_error_from_sum(a, reinterpret_cast<float *>(ctx->scratch), splits, ctx->stream));
     // the partials sit in memory every call on this GPU shares: skl_dense_backward
     // must not take them for its column sums, it reads d_prenorm / dNorm again
@@ -1162,7 +1276,8 @@ int32_t skl_dense_input_grad(skl_ctx *ctx, const skl_dense_desc *b, uint32_t bat
     g.st.ldc = b->inputs;
     const GemmPlan plan = plan_gemm(g);
     if ((r = ensure_ws(ctx, plan.bytes()))) return r;
-    if ((r = exec_gemm(ctx, g, plan, reinterpret_cast<char *>(ctx->ws)))) return r;
+    if ((r = exec_gemm(ctx, g, plan, reinterpret_cast<char *>(ctx->ws), false, nullptr, nullptr, f16 ? KEEP_A : 0)))
+        return r;
     // dX reads d_prenorm (or its fp16 copy) and W and writes dx only: column sums
     // that the error call just before left stay valid for the backward after
     // this call (a single block's dX before its optimiser step), unless dx

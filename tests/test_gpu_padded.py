@@ -18,7 +18,7 @@ import torch
 
 from oracle import oracle as O
 from soklyn_amd import abi
-from tests.helpers import FP16_TOL, rng
+from tests.helpers import FP16_TOL, f16, he_normal, rng
 from tests.test_gpu_parity import check, dev, inputs, make_pair
 
 pytestmark = pytest.mark.gpu
@@ -124,3 +124,67 @@ def test_gemm_timing_hook(ctx, M, K, N):
     assert 0.0 < ms < 1000.0, f"GEMM time {ms} ms"
     torch.cuda.synchronize()
     check("out", db.get("out"), ob.out, FP16_TOL)
+
+
+
+BLOCK_FIELDS = ("out", "predrop", "preact", "prenorm", "centered", "norm_rstd", "grad", "d_prenorm", "d_prenorm_h",
+                "d_norm_w", "d_norm_b", "w", "master_w", "dm_w", "dv_w", "b", "master_b", "dm_b", "dv_b",
+                "norm_w", "master_norm_w", "dm_norm_w", "dv_norm_w", "norm_b", "master_norm_b", "dm_norm_b",
+                "dv_norm_b")
+
+
+def test_kept_padded_d_prenorm_bit_exact(ctx, monkeypatch):
+    """An odd-width layer's d_prenorm_h is padded once per step, not twice: the GEMM that
+    pads it first (the layer's dW) keeps the copy in the context, and the hidden error of
+    the layer below, one call later, reads that copy.  Three identical C5-shaped networks
+    take the same three FeedForwardNetwork steps: A through backward_hidden (ffn.rs order)
+    and C through separate hidden_error / backward calls, both on the session context;
+    B through backward_hidden on a context made with SOKLYN_PAD_KEEP=0, whose GEMMs pad
+    into the workspace every time.  Every buffer of every block agrees bit for bit after
+    each step.  The batch shrinks and grows back (12345, 10001, 12345): a copy of
+    another batch's rows is never read."""
+    from soklyn_amd.devblock import DeviceBlock
+    monkeypatch.setenv("SOKLYN_PAD_KEEP", "0")
+    ctx_ws = abi.Context(0, 16)
+    monkeypatch.delenv("SOKLYN_PAD_KEEP")
+    ctx_ws.set_stream(torch.cuda.current_stream().cuda_stream)   # the session context's stream
+    dims, Mmax = [777, 1531, 3001, 13], 12345
+    g = rng(606)
+    ws = [he_normal(g, dims[i], dims[i + 1]) for i in range(3)]
+    hid = dict(norm=abi.NORM_LAYER, act=abi.ACT_LEAKY, leaky=0.01)
+
+    def net(c):
+        return [DeviceBlock(c, dims[i], dims[i + 1], Mmax, ws[i], half=True, master_w=ws[i],
+                            **(hid if i < 2 else dict(act=abi.ACT_IDENTITY))) for i in range(3)]
+
+    nets = {"A": net(ctx), "B": net(ctx_ws), "C": net(ctx)}
+    x = torch.from_numpy(f16(g.standard_normal((Mmax, 777)).astype(np.float32))).cuda().half()
+    t = torch.from_numpy((g.random((Mmax, 13)) > 0.5).astype(np.float32)).cuda().half()
+    for step, M in enumerate((12345, 10001, 12345), 1):
+        print(f"kept pads step {step}: batch {M}", flush=True)
+        tc = abi.train_ctx(abi.adam(), abi.adam(), M, 1e-3)
+        for name, n in nets.items():
+            cur = x[:M]
+            for blk in n:
+                cur = blk.forward(cur, M)
+            n[2].output_error(t[:M], abi.LOSS_BCE, abi.ACT_SIGMOID)
+            n[2].backward(n[1].out, tc, step)
+            if name == "C":
+                n[1].hidden_error(n[2], M)
+                n[1].backward(n[0].out, tc, step)
+                n[0].hidden_error(n[1], M)
+                n[0].backward(x[:M], tc, step)
+            else:
+                n[1].backward_hidden(n[2], n[0].out, tc, step)
+                n[0].backward_hidden(n[1], x[:M], tc, step)
+        torch.cuda.synchronize()
+        for other in ("A", "C"):
+            for i, (a, b) in enumerate(zip(nets[other], nets["B"])):
+                for f in BLOCK_FIELDS:
+                    ta, tb = getattr(a, f), getattr(b, f)
+                    if ta is None:
+                        continue
+                    bits = torch.int16 if ta.dtype == torch.float16 else torch.int32
+                    assert torch.equal(ta.view(bits), tb.view(bits)), f"step {step} net {other} layer {i} {f} differs"
+    del nets
+    ctx_ws.close()

@@ -18,8 +18,8 @@
  *  - Mode codes are the reference's ordinals (src/util/function.rs:33-39,
  *    65-72, 104-116, 153-164; LossFunc as u32 at ffn_device.rs:157).
  *  - The caller owns every buffer; no entry point allocates a tensor.  The
- *    context keeps one internal workspace (split-K partials, column partial
- *    sums) that it grows on demand.
+ *    context keeps internal buffers (split-K partials, column partial sums,
+ *    zero-padded copies of odd-width d_prenorm_h) that it grows on demand.
  *  - Return value: 0 = OK, < 0 = validation error (one code per reference
  *    Error variant, src/util/log.rs:15-99), > 0 = hipError_t.
  *  - Calls are synchronous (the reference synchronises after every launch,

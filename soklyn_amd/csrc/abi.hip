@@ -149,10 +149,12 @@ int32_t ensure_cols_splits(skl_ctx *ctx, uint32_t splits, uint32_t n) {
     return r;
 }
 
-// Room for the column sums of an error call over [rows x n]; returns the splits.
-int32_t ensure_cols(skl_ctx *ctx, uint32_t rows, uint32_t n, uint32_t *splits) {
-    *splits = err_col_splits(rows, n);
-    return ensure_cols_splits(ctx, *splits, n);
+// Room for the column sums of an error call over [rows x n]; returns the
+// splits.  src: the flat error kernel that runs (0 output error, 1 from a sum,
+// 2 skinny sum in-kernel), whose resident workgroups cap the grid.
+int32_t ensure_cols(skl_ctx *ctx, const skl_dense_desc *b, uint32_t rows, uint32_t src, uint32_t *splits) {
+    *splits = err_col_splits(rows, b->outputs, err_resident(b->dtype, src, b->outputs, b->norm != 0));
+    return ensure_cols_splits(ctx, *splits, b->outputs);
 }
 
 void record_cols(skl_ctx *ctx, const skl_dense_desc *b, uint32_t rows, uint32_t splits) {
@@ -883,7 +885,7 @@ int32_t skl_dense_output_error(skl_ctx *ctx, const skl_dense_desc *b, const void
     a.d_norm_b = b->d_norm_b;
     a.d_prenorm_h = b->dtype == SKL_F16 ? reinterpret_cast<half_t *>(b->d_prenorm_h) : nullptr;
     uint32_t splits = 0;
-    if ((r = ensure_cols(ctx, target_rows, b->outputs, &splits))) return r;
+    if ((r = ensure_cols(ctx, b, target_rows, 0, &splits))) return r;
     pad_forget(ctx, b->d_prenorm_h);
     SKL_TRY(launch_output_error(a, ctx->cols, splits, ctx->stream));
     record_cols(ctx, b, target_rows, splits);
@@ -946,7 +948,7 @@ static int32_t hidden_error_impl(skl_ctx *ctx, const skl_dense_desc *cur, const 
     // GEMM: f16(d_prenorm) and the working W for fp16 blocks).
     if (next->outputs <= 16) {
         uint32_t splits = 0;
-        if ((r = ensure_cols(ctx, batch, cur->outputs, &splits))) return r;
+        if ((r = ensure_cols(ctx, cur, batch, 2, &splits))) return r;
         const size_t esz = cur->dtype == SKL_F16 ? 2 : 4;
         const size_t a_bytes = ((size_t)batch * 16 * esz + 255) & ~(size_t)255;
         if ((r = ensure_ws(ctx, a_bytes + (size_t)cur->outputs * 16 * esz))) return r;
@@ -1027,7 +1029,7 @@ static int32_t hidden_error_impl(skl_ctx *ctx, const skl_dense_desc *cur, const 
     a.s = sum;
     a.s_ld = s_ld;
     uint32_t splits = 0;
-    if ((r = ensure_cols(ctx, batch, cur->outputs, &splits))) return r;
+    if ((r = ensure_cols(ctx, cur, batch, 1, &splits))) return r;
     SKL_TRY(launch_error_from_sum(a, ctx->cols, splits, ctx->stream));
     record_cols(ctx, cur, batch, splits);
     return SKL_OK;
@@ -1224,7 +1226,7 @@ int32_t skl_dense_error_from_sum(skl_ctx *ctx, const skl_dense_desc *b, const fl
     if ((r = zero_dnorm_tail(ctx, b, batch))) return r;
     const ErrArgs a = error_from_sum_args(b, s, batch);
     uint32_t splits = 0;
-    if ((r = ensure_cols(ctx, batch, b->outputs, &splits))) return r;
+    if ((r = ensure_cols(ctx, b, batch, 1, &splits))) return r;
     pad_forget(ctx, b->d_prenorm_h);
     SKL_TRY(launch_error_from_sum(a, ctx->cols, splits, ctx->stream));
     record_cols(ctx, b, batch, splits);
@@ -1236,7 +1238,7 @@ int32_t skl_dense_error_from_sum_noalloc(skl_ctx *ctx, const skl_dense_desc *b, 
     if (r) return r;
     if ((r = error_from_sum_checks(ctx, b, s, batch))) return r;
     SKL_CHECK(ctx->scratch, SKL_ERR_NULL_POINTER);
-    const uint32_t splits = err_col_splits(batch, b->outputs);
+    const uint32_t splits = err_col_splits(batch, b->outputs, err_resident(b->dtype, 1, b->outputs, b->norm != 0));
     SKL_CHECK((size_t)splits * 3 * b->outputs * sizeof(float) <= NOALLOC_SCRATCH_BYTES, SKL_ERR_ALLOCATION_LIMIT);
     if ((r = zero_dnorm_tail(ctx, b, batch))) return r;
     const ErrArgs a = error_from_sum_args(b, s, batch);

@@ -1105,13 +1105,18 @@ static uint32_t err_band(uint32_t n) { return (n & 3u) == 0 ? 1u : (n & 1u) ? 4u
 // Partial-sum rows of the error kernels: S row slices x err_band(n).  ~1024
 // workgroups of >= 16 rows when a band has >= 256 chunks; narrower outputs
 // leave most of a workgroup's lanes idle, so they get ~256K active lanes in
-// all, in slices of >= 4 rows (at most 4096 slices).
-uint32_t err_col_splits(uint32_t rows, uint32_t n) {
+// all, in slices of >= 4 rows (at most 4096 slices).  resident (when not 0):
+// the kernel's workgroups the GPU holds at once; a grid that would exceed it
+// gets fewer, longer slices that fill it exactly, rather than a second round
+// of a few workgroups (C5's error kernels: 1026 workgroups of which 1024 fit,
+// and 1032 of which 768 fit).
+uint32_t err_col_splits(uint32_t rows, uint32_t n, uint32_t resident) {
     const uint32_t band = err_band(n);
     const uint64_t chunks = (uint64_t)band * n / 4;   // lanes per band
+    const uint32_t gx = (uint32_t)cdiv(chunks ? chunks : 1, 256);   // workgroups per row slice
     uint32_t sp, cap;
     if (chunks >= 256) {
-        sp = cdiv(1024, cdiv(chunks, 256));
+        sp = cdiv(1024, gx);
         cap = cdiv(rows, 16);
     } else {
         sp = cdiv(262144u, chunks ? chunks : 1);
@@ -1120,7 +1125,42 @@ uint32_t err_col_splits(uint32_t rows, uint32_t n) {
     if (sp > cap) sp = cap;
     if (sp > cdiv(rows, band)) sp = cdiv(rows, band);
     if (sp > 4096) sp = 4096;
+    if (resident && (uint64_t)sp * gx > resident && resident / gx >= 1) sp = resident / gx;
     return (sp < 1 ? 1 : sp) * band;
+}
+
+// Workgroups of error_flat_kernel<T, SRC, B, NORM> per CU (its register use
+// sets it), from the runtime's occupancy calculator, once per variant.
+template <typename T, int SRC, int B, bool NORM> static uint32_t err_flat_per_cu() {
+    static const uint32_t v = [] {
+        int nb = 0;
+        const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &nb, reinterpret_cast<const void *>(&error_flat_kernel<T, SRC, B, NORM>), 256, 0);
+        return e == hipSuccess && nb > 0 ? (uint32_t)nb : 0u;
+    }();
+    return v;
+}
+template <typename T, int SRC, int B> static uint32_t err_flat_per_cu_n(bool norm) {
+    return norm ? err_flat_per_cu<T, SRC, B, true>() : err_flat_per_cu<T, SRC, B, false>();
+}
+template <typename T, int SRC> static uint32_t err_flat_per_cu_b(uint32_t band, bool norm) {
+    return band == 1 ? err_flat_per_cu_n<T, SRC, 1>(norm)
+                     : band == 2 ? err_flat_per_cu_n<T, SRC, 2>(norm) : err_flat_per_cu_n<T, SRC, 4>(norm);
+}
+template <typename T> static uint32_t err_flat_per_cu_s(uint32_t src, uint32_t band, bool norm) {
+    return src == 0 ? err_flat_per_cu_b<T, 0>(band, norm)
+                    : src == 1 ? err_flat_per_cu_b<T, 1>(band, norm) : err_flat_per_cu_b<T, 2>(band, norm);
+}
+
+uint32_t err_resident(uint32_t dtype, uint32_t src, uint32_t n, bool norm) {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        return 0;
+    const uint32_t band = err_band(n);
+    const uint32_t per_cu = dtype == 1 ? err_flat_per_cu_s<half_t>(src, band, norm)
+                                       : err_flat_per_cu_s<float>(src, band, norm);
+    return per_cu * (uint32_t)cus;
 }
 
 template <int SRC, typename T, int B>

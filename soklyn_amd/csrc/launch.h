@@ -164,7 +164,11 @@ struct ErrArgs {
 hipError_t launch_output_error(const ErrArgs &a, float *partials, uint32_t splits, hipStream_t s);
 hipError_t launch_error_from_sum(const ErrArgs &a, float *partials, uint32_t splits, hipStream_t s);
 // Partial-sum rows the error kernels write for [rows x n].
-uint32_t err_col_splits(uint32_t rows, uint32_t n);
+uint32_t err_col_splits(uint32_t rows, uint32_t n, uint32_t resident = 0);
+// Workgroups of the flat error kernel for (dtype, src: 0 output error, 1 from
+// a sum, 2 skinny sum in-kernel, n, norm != 0) the current GPU holds at once
+// (0 if unknown): err_col_splits' resident.
+uint32_t err_resident(uint32_t dtype, uint32_t src, uint32_t n, bool norm);
 // Hidden error from a next layer of at most 16 outputs without the GEMM: s =
 // A . W^T formed inside the error kernel from zero-padded copies A [rows x 16]
 // (the next layer's d_prenorm, or its fp16 copy) and W [n x 16] (its weights)

@@ -256,6 +256,7 @@ struct GemmPlan {
     bool dma;
     bool pad_a, pad_b;
     uint32_t tile;             // direct-to-LDS output tile edge (128 or 256)
+    uint32_t band;             // > 0: rows [0, band) on 256x256 tiles, the rest on 128x128 (two launches)
     uint32_t Mp, Np, Kp;       // dims the kernel runs on
     uint32_t splits;           // split-K slices of a dW (then DwPartial + reduce)
     size_t a_bytes, b_bytes, part_bytes;
@@ -301,13 +302,40 @@ uint32_t dw_dma_splits(uint32_t tiles, uint32_t Kp, uint64_t out_elems) {
 // epilogue), so it wins only where the 256x256 grid leaves most of its last
 // round empty (C5's 12544 x 1536 hidden error: 294 tiles, 2 rounds for 1.15
 // of work; 0.151 -> 0.130 ms).  Split-K grids keep 256.
-uint32_t dma_tile(Op op, uint32_t Mp, uint32_t Np, uint32_t splits) {
+// *band (forward and dX sums): a third choice, the first rows of the grid on
+// 256x256 tiles in at least two whole rounds and the remaining rows on
+// 128x128 tiles in a second launch, when that is estimated faster still.
+// Measured on C5's 12544 x 3072 forward (588 tiles): 142 us on 256x256, 141
+// on 128x128, 132 as 2 rounds + 84 tiles' worth of 128x128 rows; on its
+// 12544 x 1536 GEMMs (294 tiles) one 256x256 round plus a 128x128 launch ran
+// 3-4 us slower than 128x128 alone (a launch of fewer 128x128 workgroups than
+// CUs takes as long as a full round of them), hence two rounds at least.
+uint32_t dma_tile(Op op, uint32_t Mp, uint32_t Np, uint32_t splits, uint32_t *band) {
+    *band = 0;
     if (const uint32_t f = gemm_dma_tile_forced()) return f;
     if (splits > 1) return 256;
-    const double t256 = (double)((Mp / 256) * (Np / 256));
-    const double r256 = std::ceil(t256 / 256.0);
-    const double r128 = std::ceil(4.0 * t256 / 512.0) * 0.5 * (op == Op::DwOpt ? 1.25 : 1.15);
-    return r128 < 0.95 * r256 ? 128u : 256u;
+    const uint32_t R = Mp / 256, Cn = Np / 256;   // 256x256 tile rows and columns
+    const double f128 = op == Op::DwOpt ? 1.25 : 1.15;
+    auto rounds256 = [](double tiles) { return std::ceil(tiles / 256.0); };
+    auto rounds128 = [&](double tiles256) { return std::ceil(4.0 * tiles256 / 512.0) * 0.5 * f128; };
+    const double r256 = rounds256((double)R * Cn), r128 = rounds128((double)R * Cn);
+    const uint32_t tile = r128 < 0.95 * r256 ? 128u : 256u;
+    if (op != Op::Fwd && op != Op::InputGrad) return tile;
+    double best = tile == 128 ? r128 : r256;
+    uint32_t best_rows = 0;
+    for (uint32_t k = 2; k < (uint32_t)r256; ++k) {
+        uint32_t r1 = 256u * k / Cn;   // tile rows filling k rounds
+        if (r1 >= R) r1 = R - 1;
+        if (r1 == 0) continue;
+        const double t = rounds256((double)r1 * Cn) + rounds128((double)(R - r1) * Cn);
+        if (t < 0.95 * best) {
+            best = t;
+            best_rows = r1;
+        }
+    }
+    if (best_rows == 0) return tile;
+    *band = best_rows * 256u;
+    return 256u;
 }
 
 GemmPlan plan_gemm(const GemmLaunch &g) {
@@ -345,7 +373,7 @@ GemmPlan plan_gemm(const GemmLaunch &g) {
             p.Np = Np;
             p.Kp = Kp;
             p.splits = splits;
-            p.tile = dma_tile(g.op, Mp, Np, splits);
+            p.tile = dma_tile(g.op, Mp, Np, splits, &p.band);
             // A: k-contiguous [M x K] or m-contiguous [K x M]; B likewise with N
             p.pad_a = g.a_kcontig ? !dma_operand_ok(g.A, g.M, g.K, g.lda, 256, 128)
                                   : !dma_operand_ok(g.A, g.K, g.M, g.lda, 128, 256);
@@ -493,7 +521,24 @@ int32_t exec_gemm(skl_ctx *ctx, GemmLaunch g, const GemmPlan &p, char *ws, bool 
             g.mv = g.M;
             g.nv = g.N;
         }
-        SKL_TRY(timed_gemm(ctx, g, GemmKind::Dma));
+        if (p.band && (g.op == Op::Fwd || g.op == Op::InputGrad)) {
+            // rows [0, band) on 256x256 tiles, the rest on 128x128; the timing
+            // events, when armed, bracket both launches
+            GemmLaunch g1 = g, g2 = g;
+            g1.tile = 256;
+            g1.m_begin = 0;
+            g1.m_rows = p.band;
+            g1.time_start = ctx->gemm_start;
+            g2.tile = 128;
+            g2.m_begin = p.band;
+            g2.m_rows = p.Mp - p.band;
+            g2.time_stop = ctx->gemm_stop;
+            ctx->gemm_start = ctx->gemm_stop = nullptr;
+            SKL_TRY(launch_gemm_dma(g1, ctx->stream));
+            SKL_TRY(launch_gemm_dma(g2, ctx->stream));
+        } else {
+            SKL_TRY(timed_gemm(ctx, g, GemmKind::Dma));
+        }
     } else {
         if (p.splits > 1) {
             g.op = Op::DwPartial;

@@ -52,6 +52,7 @@ struct GemmShape {
     uint32_t k_per_split;    // reduction length per split (multiple of BK)
     uint32_t tiles_m, tiles_n;
     uint32_t mv, nv;         // 256x256 kernel on zero-padded operands: the real output extent
+    uint32_t m_base;         // direct-to-LDS kernel: first output row of the launch's tiles
 };
 
 // Workgroup barrier that orders LDS only: wait for this wave's LDS accesses,

@@ -602,8 +602,9 @@ static hipError_t run_dma_t(const GemmLaunch &g, const typename Epi::Params &p, 
     sh.lda = g.lda;
     sh.ldb = g.ldb;
     sh.k_per_split = kps;
-    sh.tiles_m = g.M / BT;
+    sh.tiles_m = (g.m_rows ? g.m_rows : g.M) / BT;
     sh.tiles_n = g.N / BT;
+    sh.m_base = g.m_begin;
     sh.mv = g.mv ? g.mv : g.M;
     sh.nv = g.nv ? g.nv : g.N;
     const dim3 grid(sh.tiles_m * sh.tiles_n, splits);
@@ -632,6 +633,13 @@ hipError_t launch_gemm_dma(const GemmLaunch &g, hipStream_t s) {
     const uint32_t kps = ((g.K / splits_req + 127) / 128) * 128;
     const uint32_t splits = (g.K + kps - 1) / kps;
     if (splits > 1 && g.op != Op::DwPartial) return hipErrorInvalidValue;
+    if (g.m_rows || g.m_begin) {
+        // a band of output rows: whole tiles inside M, not the column-sum epilogue
+        const uint32_t t = g.tile == 128 ? 128u : 256u;
+        if (g.op == Op::HiddenErr || g.m_begin % 256 || g.m_rows % t || g.m_rows == 0 ||
+            (uint64_t)g.m_begin + g.m_rows > g.M)
+            return hipErrorInvalidValue;
+    }
     const bool kk = g.a_kcontig && g.b_kcontig;
     switch (g.op) {
     case Op::Fwd:

@@ -352,7 +352,7 @@ __global__ void __launch_bounds__(64 * NW)
 
     uint32_t tm, tn;
     tile_coords(blockIdx.x, sh.tiles_m, sh.tiles_n, tm, tn);
-    const uint32_t m0 = tm * C::BM, n0 = tn * C::BN;
+    const uint32_t m0 = sh.m_base + tm * C::BM, n0 = tn * C::BN;
     const uint32_t split = blockIdx.y;
     const uint32_t kbeg = split * sh.k_per_split;
     const int kb = (int)(kbeg / C::BK);                                  // first k-tile of this split

@@ -89,6 +89,10 @@ struct GemmLaunch {
     uint32_t splits;      // split-K factor (DwPartial only; 1 otherwise)
     uint32_t tile;        // direct-to-LDS kernel: 128 (4 waves, two workgroups per CU) or 256 (0 = 256)
     uint32_t mv, nv;      // real output extent when A / B are zero-padded copies (0 = M, N)
+    // direct-to-LDS kernel: the launch covers output rows [m_begin, m_begin + m_rows)
+    // only (0, 0: all M), m_begin a multiple of 256 and m_rows of the tile edge;
+    // not for HiddenErr, whose column sums are indexed by the tile row
+    uint32_t m_begin, m_rows;
     Op op;
     FwdEpi fwd;
     OptEpi opt;

@@ -81,6 +81,44 @@ def test_input_grad_padded(ctx):
     check("input_grad", dx.cpu().numpy(), ob.input_grad(M), FP16_TOL)
 
 
+@pytest.mark.parametrize("norm,act,p", [(0, abi.ACT_SILU, 0.2), (2, abi.ACT_LEAKY, 0.1)])
+def test_forward_row_band(ctx, norm, act, p):
+    """A ragged forward whose 256x256 grid would leave most of a third round empty
+    (12345 x 3001 padded to 12544 x 3072: 588 tiles) runs output rows 0-10751 on
+    256x256 tiles and the rest on 128x128 tiles in a second launch.  Together they
+    match the oracle; without a norm the GEMM epilogue applies the activation and
+    dropout, whose masks stay bit-exact across the band boundary (the hash takes the
+    absolute row)."""
+    M, K, N = 12345, 200, 3001
+    print(f"forward row band {M}x{K}x{N} norm {norm}", flush=True)
+    ob, db = make_pair(ctx, K, N, M, seed=111 + norm, half=True, norm=norm, act=act, leaky=0.01, p=p)
+    x = inputs(112, M, K, True)
+    seed = O.scramble_seed(3, 5)
+    ob.forward(x, M, True, seed)
+    db.forward(dev(x, True), M, True, seed)
+    torch.cuda.synchronize()
+    for n in ["preact", "predrop", "out"] + (["prenorm", "centered"] if norm else []):
+        check(n, db.get(n)[:M], getattr(ob, n)[:M], FP16_TOL)
+    assert np.array_equal(db.get("mask")[:M], ob.mask[:M]), "dropout mask differs"
+
+
+def test_input_grad_row_band(ctx):
+    """dX of 12345 rows x 3001 inputs (588 padded 256x256 tiles): the banded pair of
+    launches, on padded copies of d_prenorm_h (kept in the context) and W."""
+    M, K, N = 12345, 3001, 256
+    print(f"input grad row band {M}x{K}x{N}", flush=True)
+    ob, db = make_pair(ctx, K, N, M, seed=121, half=True, act=abi.ACT_SILU)
+    x = inputs(122, M, K, True)
+    ob.forward(x, M)
+    db.forward(dev(x, True), M)
+    s = (rng(123).standard_normal((M, N)) * 512).astype(np.float32)
+    ob.error_from_sum(s, M)
+    db.error_from_sum(torch.from_numpy(s).cuda(), M)
+    dx = db.input_grad(M)
+    torch.cuda.synchronize()
+    check("input_grad", dx.cpu().numpy(), ob.input_grad(M), FP16_TOL)
+
+
 @pytest.mark.parametrize("M,K,N,norm", [
     (6000, 1000, 1531, 2),   # 24 padded tiles: split-K over the batch, partial planes reduced
     (2048, 2048, 2048, 0),   # 64 whole tiles, operands read in place: split-K only

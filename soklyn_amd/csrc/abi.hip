@@ -277,19 +277,32 @@ bool dma_operand_ok(const void *p, uint32_t rows, uint32_t cols, uint32_t ld, ui
 // kernel) plus the fp32 partial planes the slices write and the optimiser kernel
 // reads back (8 bytes per element and slice at ~5 TB/s).  A count that just
 // overflows a round loses to one fewer slice: 72 tiles take 3 slices (216
-// workgroups, one round), not 4 (288, two rounds).
-uint32_t dw_dma_splits(uint32_t tiles, uint32_t Kp, uint64_t out_elems) {
+// workgroups, one round), not 4 (288, two rounds).  *tile: the same choice
+// over 128x128 tiles (two workgroups per CU, a round of 512 taking half a
+// 256x256 round's time per slice, times 1.25 for that kernel on the dW layout)
+// when that is faster: C5's 1024 x 1536 dW (24 tiles) on 128x128 tiles in 5
+// slices, 17 us faster than 256x256 in 10; C4's 2048 x 2048 dW stays on
+// 256x256 in 4 slices (128x128 in 2: +26 us a layer).
+uint32_t dw_dma_splits(uint32_t tiles, uint32_t Kp, uint64_t out_elems, uint32_t *tile) {
     constexpr uint32_t kCus = 256;
     uint32_t best = 1;
     double best_us = 0.0;
-    for (uint32_t req = 1; req <= 16 && (req == 1 || req <= Kp / 512); ++req) {
-        const uint32_t sp = gemm_dma_splits(Kp, req);
-        const uint32_t kps = ((Kp / req + 127) / 128) * 128;   // launch_gemm_dma's slice length
-        const uint32_t rounds = (tiles * sp + kCus - 1) / kCus;
-        const double us = rounds * (kps / 128.0) * 3.4 + (sp > 1 ? sp * (double)out_elems * 8.0 / 5.0e6 : 0.0);
-        if (req == 1 || us < best_us) {
-            best = sp;
-            best_us = us;
+    *tile = 256;
+    for (uint32_t t : {256u, 128u}) {
+        const uint32_t wg = t == 256 ? tiles : 4 * tiles;      // workgroups per slice
+        const uint32_t per_round = t == 256 ? kCus : 2 * kCus;
+        const double slice_scale = t == 256 ? 1.0 : 0.5 * 1.25;
+        for (uint32_t req = 1; req <= 16 && (req == 1 || req <= Kp / 512); ++req) {
+            const uint32_t sp = gemm_dma_splits(Kp, req);
+            const uint32_t kps = ((Kp / req + 127) / 128) * 128;   // launch_gemm_dma's slice length
+            const uint32_t rounds = (wg * sp + per_round - 1) / per_round;
+            const double us = rounds * (kps / 128.0) * 3.4 * slice_scale +
+                              (sp > 1 ? sp * (double)out_elems * 8.0 / 5.0e6 : 0.0);
+            if ((t == 256 && req == 1) || us < best_us) {
+                best = sp;
+                best_us = us;
+                *tile = t;
+            }
         }
     }
     return best;
@@ -359,7 +372,8 @@ GemmPlan plan_gemm(const GemmLaunch &g) {
         const uint32_t Mp = round_up(g.M, 256), Np = round_up(g.N, 256), Kp = round_up(g.K, 128);
         // in units of 256x256 tiles whatever the kernel's tile edge
         const uint32_t tiles = (Mp / 256) * (Np / 256);
-        const uint32_t splits = dw && tiles < 160 ? dw_dma_splits(tiles, Kp, (uint64_t)Mp * Np) : 1;
+        uint32_t dw_tile = 256;
+        const uint32_t splits = dw && tiles < 160 ? dw_dma_splits(tiles, Kp, (uint64_t)Mp * Np, &dw_tile) : 1;
         const bool waste_ok = (uint64_t)Mp * Np <= (uint64_t)g.M * g.N * 3 / 2;
         // the kernel's operand offsets are 32-bit
         const uint64_t a_span = g.a_kcontig ? (uint64_t)Mp * (g.lda > Kp ? g.lda : Kp)
@@ -367,13 +381,16 @@ GemmPlan plan_gemm(const GemmLaunch &g) {
         const uint64_t b_span = g.b_kcontig ? (uint64_t)Np * (g.ldb > Kp ? g.ldb : Kp)
                                             : (uint64_t)Kp * (g.ldb > Np ? g.ldb : Np);
         const bool offsets_ok = a_span * 2 < (1ull << 32) && b_span * 2 < (1ull << 32);
-        if (waste_ok && offsets_ok && tiles * splits >= 192) {
+        // enough workgroups to fill the GPU: 192 of 256x256, or 384 of 128x128 (two per CU)
+        const uint32_t fill = dw_tile == 128 ? 4 * tiles * splits / 2 : tiles * splits;
+        if (waste_ok && offsets_ok && fill >= 192) {
             p.dma = true;
             p.Mp = Mp;
             p.Np = Np;
             p.Kp = Kp;
             p.splits = splits;
             p.tile = dma_tile(g.op, Mp, Np, splits, &p.band);
+            if (dw && dw_tile == 128 && !gemm_dma_tile_forced()) p.tile = 128;
             // A: k-contiguous [M x K] or m-contiguous [K x M]; B likewise with N
             p.pad_a = g.a_kcontig ? !dma_operand_ok(g.A, g.M, g.K, g.lda, 256, 128)
                                   : !dma_operand_ok(g.A, g.K, g.M, g.lda, 128, 256);

@@ -255,7 +255,7 @@ struct GemmPlan {
     bool skinny;               // N <= 16: the streaming kernels (forward, dW partials)
     bool dma;
     bool pad_a, pad_b;
-    uint32_t tile;             // direct-to-LDS output tile edge (128 or 256)
+    uint32_t tile;             // direct-to-LDS output tile edge (128 or 256); 128: fp32 dW on 128x128 tiles
     uint32_t band;             // > 0: rows [0, band) on 256x256 tiles, the rest on 128x128 (two launches)
     uint32_t Mp, Np, Kp;       // dims the kernel runs on
     uint32_t splits;           // split-K slices of a dW (then DwPartial + reduce)
@@ -405,8 +405,16 @@ GemmPlan plan_gemm(const GemmLaunch &g) {
     }
     // register-staged kernels; split-K for small dW grids
     if (dw) {
-        const uint32_t tiles = gemm_tiles(g.dtype, g.M, g.N);
+        uint32_t tiles = gemm_tiles(g.dtype, g.M, g.N);
         const uint32_t bk = gemm_bk(g.dtype);
+        // fp32: 128x128 tiles split over the batch rather than the 64x64 tiles a
+        // small grid would otherwise get (C2's 1024 x 1024 dW over 4096 rows: 4
+        // slices of 64 tiles, 103 -> 77 us, against 256 whole 64x64 tiles)
+        const uint32_t t128 = ((g.M + 127) / 128) * ((g.N + 127) / 128);
+        if (g.dtype == SKL_F32 && t128 < 160 && g.K >= 8 * 4 * bk) {
+            tiles = t128;
+            p.tile = 128;
+        }
         if (tiles < 160 && g.K >= 8 * bk) {
             uint32_t splits = (256 + tiles - 1) / tiles;
             const uint32_t max_splits = g.K / (4 * bk);
@@ -564,6 +572,7 @@ int32_t exec_gemm(skl_ctx *ctx, GemmLaunch g, const GemmPlan &p, char *ws, bool 
             g.st.split_stride = (uint64_t)M * N;
             g.st.ldc = N;
         }
+        g.tile = p.tile;
         SKL_TRY(timed_gemm(ctx, g, GemmKind::Staged));
     }
     if (p.splits > 1) {

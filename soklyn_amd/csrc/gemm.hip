@@ -1065,7 +1065,7 @@ hipError_t launch_gemm(const GemmLaunch &g, hipStream_t s) {
         return dispatch_op<CfgH128>(g, s);
     }
     const uint32_t t128 = ((g.M + 127) / 128) * ((g.N + 127) / 128);
-    return t128 >= 192 ? dispatch_op<CfgF128>(g, s) : dispatch_op<CfgF64>(g, s);
+    return t128 >= 192 || g.tile == 128 ? dispatch_op<CfgF128>(g, s) : dispatch_op<CfgF64>(g, s);
 }
 
 }  // namespace skl

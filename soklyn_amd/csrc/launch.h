@@ -87,7 +87,8 @@ struct GemmLaunch {
     bool a_kcontig, b_kcontig;
     const void *A, *B;
     uint32_t splits;      // split-K factor (DwPartial only; 1 otherwise)
-    uint32_t tile;        // direct-to-LDS kernel: 128 (4 waves, two workgroups per CU) or 256 (0 = 256)
+    uint32_t tile;        // direct-to-LDS kernel: 128 (4 waves, two workgroups per CU) or 256 (0 = 256);
+                          // fp32 register-staged kernel: 128 asks for 128x128 tiles on any grid
     uint32_t mv, nv;      // real output extent when A / B are zero-padded copies (0 = M, N)
     // direct-to-LDS kernel: the launch covers output rows [m_begin, m_begin + m_rows)
     // only (0, 0: all M), m_begin a multiple of 256 and m_rows of the tile edge;

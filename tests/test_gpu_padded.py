@@ -226,3 +226,40 @@ def test_kept_padded_d_prenorm_bit_exact(ctx, monkeypatch):
                     assert torch.equal(ta.view(bits), tb.view(bits)), f"step {step} net {other} layer {i} {f} differs"
     del nets
     ctx_ws.close()
+
+
+def test_kept_pad_input_grad_then_backward_bit_exact(ctx, monkeypatch):
+    """A single ragged block's step in bench.py's order: error_from_sum, input_grad (its
+    dX GEMM pads d_prenorm_h as A and keeps the copy), backward (the dW GEMM reads that
+    copy as B one call later).  Against a context with SOKLYN_PAD_KEEP=0 (every GEMM
+    pads into the workspace), dx and every buffer agree bit for bit over two steps."""
+    from soklyn_amd.devblock import DeviceBlock
+    monkeypatch.setenv("SOKLYN_PAD_KEEP", "0")
+    ctx_ws = abi.Context(0, 16)
+    monkeypatch.delenv("SOKLYN_PAD_KEEP")
+    ctx_ws.set_stream(torch.cuda.current_stream().cuda_stream)
+    M, K, N = 12345, 1531, 3001   # dX: 294 tiles on the direct-to-LDS kernel, d_prenorm_h padded as A
+    g = rng(707)
+    w = he_normal(g, K, N)
+    blocks = [DeviceBlock(c, K, N, M, w, half=True, master_w=w, act=abi.ACT_SILU) for c in (ctx, ctx_ws)]
+    x = dev(inputs(708, M, K, True), True)
+    s = torch.from_numpy((g.standard_normal((M, N)) * 512).astype(np.float32)).cuda()
+    for step in (1, 2):
+        print(f"kept pad dX -> dW step {step}", flush=True)
+        tc = abi.train_ctx(abi.adam(), abi.adam(), M, 1e-3)
+        dxs = []
+        for b in blocks:
+            b.forward(x, M)
+            b.error_from_sum(s, M)
+            dxs.append(b.input_grad(M))
+            b.backward(x, tc, step)
+        torch.cuda.synchronize()
+        assert torch.equal(dxs[0].view(torch.int32), dxs[1].view(torch.int32)), f"step {step} dx differs"
+        for f in BLOCK_FIELDS:
+            ta, tb = getattr(blocks[0], f), getattr(blocks[1], f)
+            if ta is None:
+                continue
+            bits = torch.int16 if ta.dtype == torch.float16 else torch.int32
+            assert torch.equal(ta.view(bits), tb.view(bits)), f"step {step} {f} differs"
+    del blocks
+    ctx_ws.close()

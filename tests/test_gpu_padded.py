@@ -81,7 +81,8 @@ def test_input_grad_padded(ctx):
     check("input_grad", dx.cpu().numpy(), ob.input_grad(M), FP16_TOL)
 
 
-@pytest.mark.parametrize("norm,act,p", [(0, abi.ACT_SILU, 0.2), (2, abi.ACT_LEAKY, 0.1)])
+@pytest.mark.parametrize("norm,act,p", [(0, abi.ACT_SILU, 0.2), (1, abi.ACT_MISH, 0.1), (2, abi.ACT_LEAKY, 0.1),
+                                        (3, abi.ACT_SIGMOID, 0.0)])
 def test_forward_row_band(ctx, norm, act, p):
     """A ragged forward whose 256x256 grid would leave most of a third round empty
     (12345 x 3001 padded to 12544 x 3072: 588 tiles) runs output rows 0-10751 on

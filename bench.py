@@ -1,6 +1,6 @@
 """DenseBlock hot-path benchmark on one MI355X (default: the headline).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3|c2|c4|c5] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--settle-ms S] [--config c3|c2|c4|c5] [--no-cpu]
     python bench.py --copy-probe MIB      (counter calibration copy only)
 
 Every step goes through the C ABI (libsoklyn_hip.so) with its inputs resident in HBM.
@@ -17,6 +17,11 @@ MLPs (c4 = config 4, c5 = config 5), one step = FeedForwardNetwork's train step
 layer, then for each lower layer the hidden error from the updated layer above
 followed by its own backward;
   algorithmic work = forward and dW of every layer + dX of layers 2..L.
+Before the W warm-up steps the step runs untimed for at least --settle-ms of
+wall time (default 250): under load the GPU's clocks take ~50 ms to reach their
+steady state, and with few warm-up steps the timed steps would fall in that
+ramp (C3: 855 TFLOP/s with 5 warm-up steps, 885-930 once settled).  The timed
+region is still exactly K steps; the line reports the settle time and steps.
 Prints one JSON line.
 """
 from __future__ import annotations
@@ -72,6 +77,8 @@ def parse():
     # ~50 ms of load before the timed steps: the GPU reaches its steady clocks only
     # after that (C3: 855 TFLOP/s with 5 warm-up steps, 885-895 with 50 or 200)
     p.add_argument("--warmup", type=int, default=50)
+    p.add_argument("--settle-ms", type=float, default=250.0,
+                   help="untimed steps before the warm-up until this much wall time has passed (clock ramp)")
     p.add_argument("--config", default="c3", choices=sorted(CONFIGS))
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-rows", type=int, default=0, help="rows of the CPU baseline sample (0 = auto)")
@@ -368,6 +375,12 @@ def main():
     gevs = [timing_events(len(gemms)) for _ in range(args.steps)]
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    settle_steps, t_settle = 0, time.perf_counter()
+    while (time.perf_counter() - t_settle) * 1e3 < args.settle_ms:
+        for _ in range(4):
+            bench.step()
+        settle_steps += 4
+        torch.cuda.synchronize()
     for _ in range(args.warmup):
         bench.step()
     torch.cuda.synchronize()
@@ -413,6 +426,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle": {"ms": args.settle_ms, "steps": settle_steps},
         "ms_per_step": round(ms, 4),
         "higher_is_better": True,
         "scaling": "weak",

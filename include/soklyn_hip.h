@@ -24,7 +24,17 @@
  *    Error variant, src/util/log.rs:15-99), > 0 = hipError_t.
  *  - Calls are synchronous (the reference synchronises after every launch,
  *    ffn_device.rs:75,110,136,189,228,355,436) unless skl_ctx_set_sync(ctx, 0)
- *    is called; then work is only ordered on the context's stream.
+ *    is called; then work is only ordered on the context's stream.  A call on a
+ *    stream that is being captured into a HIP graph skips that synchronisation
+ *    (it would end the capture); capturing also needs a caller-owned stream
+ *    (skl_ctx_set_stream) and a call that grows none of the context's buffers
+ *    (skl_dense_error_from_sum_noalloc, or buffers an earlier call of the same
+ *    shapes already grew).
+ *  - The context keeps padded copies of d_prenorm_h and column sums of
+ *    d_prenorm between calls.  An error entry point on any context that
+ *    rewrites those buffers makes them stale; a caller that rewrites d_prenorm,
+ *    d_prenorm_h or dNorm with its own kernels between two calls must make one
+ *    more entry-point call on the context in between (any call does).
  */
 #ifndef SOKLYN_HIP_H
 #define SOKLYN_HIP_H
@@ -196,7 +206,8 @@ int32_t skl_dense_error_from_sum(skl_ctx *ctx, const skl_dense_desc *blk, const 
 
 /* skl_dense_error_from_sum that allocates nothing.  No counterpart in the
  * reference: for callers that cannot call hipMalloc (code under HIP graph
- * capture, tight serving loops, harnesses that forbid allocation).  Same checks
+ * capture, on a caller-owned stream; tight serving loops; harnesses that forbid
+ * allocation).  Same checks
  * and same outputs as skl_dense_error_from_sum, bit for bit; the error kernel's
  * column partial sums go to a 16 MiB device array the library holds per GPU
  * (looked up in skl_ctx_create) instead of the context's grown buffer.

@@ -11,6 +11,7 @@
 
 #include <cmath>
 #include <mutex>
+#include <unordered_map>
 
 #include <hip/hip_runtime.h>
 
@@ -29,6 +30,7 @@ struct ColSums {
     const float *dp, *dnw, *dnb;
     uint32_t rows, n, splits, norm;
     uint64_t call;
+    uint64_t gen;        // rewrite_gen(dp) when made
     bool valid;
 };
 
@@ -48,6 +50,7 @@ struct PadCopy {
     const void *src;   // the d_prenorm_h it mirrors
     uint32_t rows, n, ld;
     uint64_t call;
+    uint64_t gen;      // rewrite_gen(src) when made
     bool valid;
 };
 
@@ -93,9 +96,15 @@ int32_t hip_status(hipError_t e) { return e == hipSuccess ? SKL_OK : (int32_t)e;
         if (!(cond)) return (code);                                    \
     } while (0)
 
+// Synchronous calls wait for their stream, except on a stream that is being
+// captured into a HIP graph (a synchronize there would invalidate the capture).
 int32_t finish(skl_ctx *ctx) {
     SKL_TRY(hipGetLastError());
-    if (ctx->sync) SKL_TRY(hipStreamSynchronize(ctx->stream));
+    if (ctx->sync) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        SKL_TRY(hipStreamIsCapturing(ctx->stream, &cs));
+        if (cs == hipStreamCaptureStatusNone) SKL_TRY(hipStreamSynchronize(ctx->stream));
+    }
     return SKL_OK;
 }
 
@@ -157,6 +166,31 @@ int32_t ensure_cols(skl_ctx *ctx, const skl_dense_desc *b, uint32_t rows, uint32
     return ensure_cols_splits(ctx, *splits, b->outputs);
 }
 
+// Rewrites of a block's d_prenorm / d_prenorm_h by the error entry points,
+// counted per buffer address over the whole process: a kept padded copy or
+// column-sum set remembers the count of its source when it was made and is
+// stale once an error call on any context has rewritten that buffer since.
+std::mutex g_gen_mu;
+std::unordered_map<const void *, uint64_t> g_gen;
+
+uint64_t rewrite_gen(const void *p) {
+    std::lock_guard<std::mutex> lock(g_gen_mu);
+    const auto it = g_gen.find(p);
+    return it == g_gen.end() ? 0 : it->second;
+}
+
+void pad_forget(skl_ctx *ctx, const void *src);
+
+// An error entry point is about to rewrite b's d_prenorm (and d_prenorm_h).
+void note_rewrite(skl_ctx *ctx, const skl_dense_desc *b) {
+    {
+        std::lock_guard<std::mutex> lock(g_gen_mu);
+        ++g_gen[b->d_prenorm];
+        if (b->d_prenorm_h) ++g_gen[b->d_prenorm_h];
+    }
+    if (b->d_prenorm_h) pad_forget(ctx, b->d_prenorm_h);
+}
+
 void record_cols(skl_ctx *ctx, const skl_dense_desc *b, uint32_t rows, uint32_t splits) {
     ColSums &c = ctx->cs;
     c.dp = b->d_prenorm;
@@ -167,6 +201,7 @@ void record_cols(skl_ctx *ctx, const skl_dense_desc *b, uint32_t rows, uint32_t 
     c.splits = splits;
     c.norm = b->norm;
     c.call = ctx->calls;
+    c.gen = rewrite_gen(b->d_prenorm);
     c.valid = true;
 }
 
@@ -178,7 +213,8 @@ bool overlaps(const void *a, size_t an, const void *b, size_t bn) {
 bool cols_match(const skl_ctx *ctx, const skl_dense_desc *b, uint32_t rows) {
     const ColSums &c = ctx->cs;
     return c.valid && c.call + 1 >= ctx->calls && c.dp == b->d_prenorm && c.rows == rows && c.n == b->outputs &&
-           c.norm == b->norm && (b->norm == SKL_NORM_DISABLED || (c.dnw == b->d_norm_w && c.dnb == b->d_norm_b));
+           c.norm == b->norm && (b->norm == SKL_NORM_DISABLED || (c.dnw == b->d_norm_w && c.dnb == b->d_norm_b)) &&
+           c.gen == rewrite_gen(b->d_prenorm);
 }
 
 uint32_t round_up(uint32_t v, uint32_t m) { return (v + m - 1) / m * m; }
@@ -192,7 +228,8 @@ void pad_forget(skl_ctx *ctx, const void *src) {
 // The current padded copy of a GEMM operand stored as [rows x cols] at pitch ld, if any.
 const PadCopy *pad_copy_of(const skl_ctx *ctx, const void *p, uint32_t rows, uint32_t cols, uint32_t ld) {
     for (const PadCopy &c : ctx->pads)
-        if (c.valid && c.src == p && c.rows == rows && c.n == cols && ld == cols && c.call + 1 >= ctx->calls)
+        if (c.valid && c.src == p && c.rows == rows && c.n == cols && ld == cols && c.call + 1 >= ctx->calls &&
+            c.gen == rewrite_gen(p))
             return &c;
     return nullptr;
 }
@@ -231,6 +268,7 @@ int32_t pad_keep(skl_ctx *ctx, const void *p, uint32_t rows, uint32_t cols, uint
     c->n = cols;
     c->ld = ld_p;
     c->call = ctx->calls;
+    c->gen = rewrite_gen(p);
     c->valid = true;
     *out = c;
     return SKL_OK;
@@ -527,9 +565,12 @@ int32_t exec_gemm(skl_ctx *ctx, GemmLaunch g, const GemmPlan &p, char *ws, bool 
         g.nv = full_out ? p.Np : N;
         g.tile = p.tile;
         if (vec && g.op == Op::DwOpt && p.splits == 1) {
-            // the bias / norm-parameter update rides in the fused kernel's launch
+            // the bias / norm-parameter update rides in the fused kernel's launch;
+            // its 64 NW threads take cpb columns each with the lanes per column of a
+            // 256-thread vec_opt_kernel, so every column is summed in the same order
+            // as there (and in the split-K reduction's launch)
             g.opt.vec = *vec;
-            g.opt.vec.cpb = vec_opt_cpb(vec->splits);
+            g.opt.vec.cpb = vec_opt_cpb(vec->splits) * (p.tile == 128 ? 1u : 2u);
             g.opt.vec_blocks = (vec->n + g.opt.vec.cpb - 1) / g.opt.vec.cpb;
             if (vec_done) *vec_done = true;
         }
@@ -957,7 +998,7 @@ int32_t skl_dense_output_error(skl_ctx *ctx, const skl_dense_desc *b, const void
     a.d_prenorm_h = b->dtype == SKL_F16 ? reinterpret_cast<half_t *>(b->d_prenorm_h) : nullptr;
     uint32_t splits = 0;
     if ((r = ensure_cols(ctx, b, target_rows, 0, &splits))) return r;
-    pad_forget(ctx, b->d_prenorm_h);
+    note_rewrite(ctx, b);
     SKL_TRY(launch_output_error(a, ctx->cols, splits, ctx->stream));
     record_cols(ctx, b, target_rows, splits);
     return finish(ctx);
@@ -1011,7 +1052,7 @@ static int32_t hidden_error_impl(skl_ctx *ctx, const skl_dense_desc *cur, const 
     a.d_prenorm_h = cur->dtype == SKL_F16 ? reinterpret_cast<half_t *>(cur->d_prenorm_h) : nullptr;
     const void *next_dp = cur->dtype == SKL_F16 ? next->d_prenorm_h : next->d_prenorm;
     const uint32_t keep = cur->dtype == SKL_F16 ? KEEP_A : 0;   // next_dp is a d_prenorm_h
-    pad_forget(ctx, cur->d_prenorm_h);
+    note_rewrite(ctx, cur);
 
     // A next layer of at most 16 outputs: its GEMM would pad k to 128, so the
     // error kernel forms s = next.d_prenorm . next.W^T itself, per element, from
@@ -1298,7 +1339,7 @@ int32_t skl_dense_error_from_sum(skl_ctx *ctx, const skl_dense_desc *b, const fl
     const ErrArgs a = error_from_sum_args(b, s, batch);
     uint32_t splits = 0;
     if ((r = ensure_cols(ctx, b, batch, 1, &splits))) return r;
-    pad_forget(ctx, b->d_prenorm_h);
+    note_rewrite(ctx, b);
     SKL_TRY(launch_error_from_sum(a, ctx->cols, splits, ctx->stream));
     record_cols(ctx, b, batch, splits);
     return finish(ctx);
@@ -1314,7 +1355,7 @@ int32_t skl_dense_error_from_sum_noalloc(skl_ctx *ctx, const skl_dense_desc *b, 
     if ((r = zero_dnorm_tail(ctx, b, batch))) return r;
     const ErrArgs a = error_from_sum_args(b, s, batch);
     // every split writes all of its partial-sum rows: nothing in the scratch needs clearing
-    pad_forget(ctx, b->d_prenorm_h);
+    note_rewrite(ctx, b);
     SKL_TRY(launch_error_from_sum(a, reinterpret_cast<float *>(ctx->scratch), splits, ctx->stream));
     // the partials sit in memory every call on this GPU shares: skl_dense_backward
     // must not take them for its column sums, it reads d_prenorm / dNorm again

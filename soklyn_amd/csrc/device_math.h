@@ -213,9 +213,18 @@ struct OptParams {
 
 // backward.cu:105-154, one element.  p, v, m are the fp32 master and moments
 // (in/out); grad_acc is the raw accumulated gradient, already / LOSS_SCALE.
+// FAST (fp16 blocks): Adam's bias corrections and step with the hardware
+// reciprocal and square root (v_rcp_f32, v_sqrt_f32, ~1 ulp each), which moves
+// the update by a few fp32 ulp and took C3's dW + Adam 0.288 -> 0.283 ms; fp32
+// blocks keep the reference's IEEE quotients and sqrtf (it is built without
+// fast math) so their masters follow it to the last bit the formula allows.
+template <bool FAST>
 __device__ __forceinline__ void optimiser_step(float &p, float &v, float &mm, float grad_acc, float inv_m,
                                                float lr, float clamp, const OptParams &o,
                                                uint32_t regularisation, float regu_coeff, bool apply_regul) {
+    // no fused multiply-adds: every kernel that applies the step (the fused dW
+    // epilogue, the split-K reduction, the parameter update) rounds it alike
+#pragma clang fp contract(off)
     const float val = grad_acc * inv_m;
     if (apply_regul) {
         const float sign = p > 0.0f ? 1.0f : (p < 0.0f ? -1.0f : 0.0f);  // math.cuh:60-66 on master
@@ -233,12 +242,16 @@ __device__ __forceinline__ void optimiser_step(float &p, float &v, float &mm, fl
         const float dvl = o.beta2 * v + (1.0f - o.beta2) * val * val;
         mm = dml;
         v = dvl;
-        // hardware reciprocal and square root (v_rcp_f32, v_sqrt_f32, ~1 ulp
-        // each) for the reference's IEEE quotients and sqrtf: the update moves
-        // by a few fp32 ulp, and dW + Adam's epilogue by 2% of its time
-        const float mc = dml * __builtin_amdgcn_rcpf(o.bc1);
-        const float vc = dvl * __builtin_amdgcn_rcpf(o.bc2);
-        float u = lr * (mc * __builtin_amdgcn_rcpf(__builtin_amdgcn_sqrtf(vc) + o.epsilon));
+        float u;
+        if constexpr (FAST) {
+            const float mc = dml * __builtin_amdgcn_rcpf(o.bc1);
+            const float vc = dvl * __builtin_amdgcn_rcpf(o.bc2);
+            u = lr * (mc * __builtin_amdgcn_rcpf(__builtin_amdgcn_sqrtf(vc) + o.epsilon));
+        } else {
+            const float mc = dml / o.bc1;
+            const float vc = dvl / o.bc2;
+            u = lr * (mc / (sqrtf(vc) + o.epsilon));
+        }
         u = fminf(fmaxf(u, -clamp), clamp);
         p -= u;
     }

@@ -49,8 +49,28 @@ hipError_t launch_fill(void *dst, uint32_t dtype, float v, size_t n, hipStream_t
     return hipGetLastError();
 }
 
+// f32 -> f16 (round to nearest even) four elements per thread: 16-byte loads,
+// 8-byte stores (n4 = n / 4 groups; the caller casts the tail).
+__global__ void cast_f32_f16_x4_kernel(const f32x4 *src, uint64_t *dst, uint64_t n4) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (uint64_t)gridDim.x * blockDim.x) {
+        const f32x4 v = __builtin_nontemporal_load(src + i);
+        half_t h[4] = {(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
+        dst[i] = __builtin_bit_cast(uint64_t, h);
+    }
+}
+
 hipError_t launch_cast(const void *src, uint32_t sdt, void *dst, uint32_t ddt, size_t n, hipStream_t s) {
     if (n == 0) return hipSuccess;
+    if (sdt == 0 && ddt == 1 && n >= 4 && (reinterpret_cast<uintptr_t>(src) & 15u) == 0 &&
+        (reinterpret_cast<uintptr_t>(dst) & 7u) == 0) {
+        const uint64_t n4 = n / 4;
+        hipLaunchKernelGGL(cast_f32_f16_x4_kernel, dim3((uint32_t)std::min<uint64_t>((n4 + 255) / 256, 8192)),
+                           dim3(256), 0, s, (const f32x4 *)src, (uint64_t *)dst, n4);
+        if (n % 4)
+            hipLaunchKernelGGL((cast_kernel<float, half_t>), dim3(1), dim3(64), 0, s, (const float *)src + 4 * n4,
+                               (half_t *)dst + 4 * n4, (uint64_t)(n % 4));
+        return hipGetLastError();
+    }
     if (sdt == 0 && ddt == 1)
         hipLaunchKernelGGL((cast_kernel<float, half_t>), grid_for(n, 256), dim3(256), 0, s, (const float *)src,
                            (half_t *)dst, (uint64_t)n);
@@ -1430,16 +1450,16 @@ template <typename T, int VW> __global__ void __launch_bounds__(256) dw_reduce_o
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 float pj = p[j], vj = dv[j], mj = dm[j];
-                optimiser_step(pj, vj, mj, sum[j] * kLossScaleInv, e.inv_m, e.lr, e.clamp, e.opt, e.regularisation,
-                               e.regu_coeff, true);
+                optimiser_step<sizeof(T) == 2>(pj, vj, mj, sum[j] * kLossScaleInv, e.inv_m, e.lr, e.clamp, e.opt,
+                                               e.regularisation, e.regu_coeff, true);
                 p[j] = pj;
                 dv[j] = vj;
                 dm[j] = mj;
             }
             if (e.param) store4<T>(e.param, idx, p);
         } else {
-            optimiser_step(p, dv, dm, sum * kLossScaleInv, e.inv_m, e.lr, e.clamp, e.opt, e.regularisation,
-                           e.regu_coeff, true);
+            optimiser_step<sizeof(T) == 2>(p, dv, dm, sum * kLossScaleInv, e.inv_m, e.lr, e.clamp, e.opt,
+                                           e.regularisation, e.regu_coeff, true);
             if (e.param) stv<T>(e.param, idx, from_f32<T>(p));
         }
         *reinterpret_cast<V *>(e.master + idx) = p;

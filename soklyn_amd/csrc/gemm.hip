@@ -249,8 +249,8 @@ template <typename T> struct EpiOptK {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             float pj = p[j], vj = dv[j], mj = dm[j];
-            optimiser_step(pj, vj, mj, v[j] * kLossScaleInv, e.inv_m, e.lr, e.clamp, e.opt, e.regularisation,
-                           e.regu_coeff, true);
+            optimiser_step<sizeof(T) == 2>(pj, vj, mj, v[j] * kLossScaleInv, e.inv_m, e.lr, e.clamp, e.opt,
+                                           e.regularisation, e.regu_coeff, true);
             p[j] = pj; dv[j] = vj; dm[j] = mj;
         }
         *reinterpret_cast<floatx4 *>(e.master + idx) = p;
@@ -273,8 +273,8 @@ template <typename T> struct EpiOptK {
                                                   uint32_t) {
         const uint64_t idx = (uint64_t)m * e.ldc + n;
         float pj = e.master[idx], vj = e.dv[idx], mj = e.dm[idx];
-        optimiser_step(pj, vj, mj, v * kLossScaleInv, e.inv_m, e.lr, e.clamp, e.opt, e.regularisation, e.regu_coeff,
-                       true);
+        optimiser_step<sizeof(T) == 2>(pj, vj, mj, v * kLossScaleInv, e.inv_m, e.lr, e.clamp, e.opt,
+                                       e.regularisation, e.regu_coeff, true);
         e.master[idx] = pj;
         e.dv[idx] = vj;
         e.dm[idx] = mj;
@@ -295,8 +295,8 @@ template <typename T> struct EpiOptK {
                 if (c >= sh.N) break;
                 const uint64_t idx = base + c;
                 float pj = e.master[idx], vj = e.dv[idx], mj = e.dm[idx];
-                optimiser_step(pj, vj, mj, v[j] * kLossScaleInv, e.inv_m, e.lr, e.clamp, e.opt, e.regularisation,
-                               e.regu_coeff, true);
+                optimiser_step<sizeof(T) == 2>(pj, vj, mj, v[j] * kLossScaleInv, e.inv_m, e.lr, e.clamp, e.opt,
+                                               e.regularisation, e.regu_coeff, true);
                 e.master[idx] = pj;
                 e.dv[idx] = vj;
                 e.dm[idx] = mj;

@@ -58,7 +58,7 @@ template <typename T, int NT = 256> __device__ __forceinline__ void vec_opt_bloc
         if (!a.enabled[k]) continue;
         const float s = red[k][cl];
         float p = a.master[k][col], v = a.dv[k][col], mm = a.dm[k][col];
-        optimiser_step(p, v, mm, s * kLossScaleInv, a.inv_m, a.lr, a.clamp, a.opt[k], 0, 0.0f, false);
+        optimiser_step<sizeof(T) == 2>(p, v, mm, s * kLossScaleInv, a.inv_m, a.lr, a.clamp, a.opt[k], 0, 0.0f, false);
         a.master[k][col] = p;
         a.dv[k][col] = v;
         a.dm[k][col] = mm;

@@ -85,6 +85,24 @@ def check(name, a, r, tol) -> float:
     return nw
 
 
+def check_sum_bound(name, a, r, scale, tol=FP32_TOL) -> float:
+    """fp32 GEMM outputs element by element: |a - r| <= tol * scale, where scale is the
+    element's sum over k of |x_k w_k| (plus |bias|): the bound the rounding of any
+    order of the k additions stays within (n u scale, u = 2^-24, far below 1e-4 for
+    these k), so unlike |a - r| / |r| it does not fail on outputs that cancel to near
+    zero, and unlike the normwise metric it holds for every element."""
+    a = np.asarray(a, np.float64)
+    r = np.asarray(r, np.float64)
+    scale = np.asarray(scale, np.float64)
+    assert a.shape == r.shape == scale.shape, f"{name}: shapes {a.shape} {r.shape} {scale.shape}"
+    worst = float(np.max(np.abs(a - r) / np.maximum(scale, np.finfo(np.float64).tiny)))
+    RECORDS.append({"test": os.environ.get("PYTEST_CURRENT_TEST", "").split(" ")[0], "name": name + " (sum bound)",
+                    "normwise": None, "elementwise": worst, "tol": tol, "ew_tol": tol})
+    print(f"  {name}: max |a - r| / sum|terms| {worst:.2e}  (gate {tol:.0e} per element)", flush=True)
+    assert worst <= tol, f"{name}: element error {worst:.3e} of its summation scale > {tol:.0e}"
+    return worst
+
+
 def check_adam_update(name, w0, w1, dm, dv, lr, step, ref_update, ref_dm, beta1=0.9, beta2=0.999, eps=1e-8):
     """The Adam step on the fp32 master (backward.cu:133-147): w1 - w0 must equal
     -lr * (dm / (1 - beta1^t)) / (sqrt(dv / (1 - beta2^t)) + eps) computed from the

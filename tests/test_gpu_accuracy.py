@@ -22,7 +22,11 @@ from tests.helpers import elementwise, he_normal, normwise, rng
 
 pytestmark = pytest.mark.gpu
 
-SHAPES = [(4096, 1024, 1024), (2048, 256, 2048), (4100, 2048, 10), (1000, 777, 1531), (130, 40, 3001)]
+# (1100, 777, 1531) and (2500, 300, 130): ragged outputs at batches of 1024 and more, whose fp32
+# dW runs on 128x128 register-staged tiles split over the batch (slices that are not a multiple
+# of 32 rows) and the reduction kernel
+SHAPES = [(4096, 1024, 1024), (2048, 256, 2048), (4100, 2048, 10), (1000, 777, 1531), (130, 40, 3001),
+          (1100, 777, 1531), (2500, 300, 130)]
 
 
 def judge(name, dev, orc, exact):

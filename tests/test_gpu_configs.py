@@ -29,7 +29,7 @@ import torch
 from oracle import oracle as O
 from soklyn_amd import abi
 from soklyn_amd.devblock import DeviceBlock
-from tests.helpers import FP16_TOL, FP32_TOL, check, check_adam_update, f16, he_normal, rng
+from tests.helpers import FP16_TOL, FP32_TOL, check, check_adam_update, check_sum_bound, f16, he_normal, rng
 from tests.test_gpu_ffn import build_net
 
 pytestmark = pytest.mark.gpu
@@ -74,16 +74,27 @@ def single_block_step(ctx, M, K, N, half, act, opt_o, opt_d, lr):
     dx = db.input_grad(M)
     db.backward(xd, abi.train_ctx(opt_d, opt_d, M, lr), 1)
     torch.cuda.synchronize()
+    ob.x_, ob.s_ = x, s
     return ob, db, dx.cpu().numpy(), dx_ref, w
 
 
 def test_c2_fp32_full_size(ctx):
     tol = FP32_TOL
-    ob, db, dx, dx_ref, _ = single_block_step(ctx, 4096, 1024, 1024, False, abi.ACT_RELU, O.Optimiser.sgd(0.0),
-                                              abi.sgd(0.0), 1e-2)
+    M, K, N = 4096, 1024, 1024
+    ob, db, dx, dx_ref, w0 = single_block_step(ctx, M, K, N, False, abi.ACT_RELU, O.Optimiser.sgd(0.0),
+                                               abi.sgd(0.0), 1e-2)
     for n in ("grad", "d_prenorm", "dv_w", "dv_b", "w", "b"):
         check(n, db.get(n), getattr(ob, n), tol)
     check("dX", dx, dx_ref, tol)
+    # element by element, against the summation-error scale of each GEMM output (the sum
+    # over k of |a_k b_k|): the north star's 1e-4 relative, with a denominator that the
+    # order of the additions cannot exceed
+    absx, absw = np.abs(ob.x_).astype(np.float64), np.abs(w0).astype(np.float64)
+    check_sum_bound("preact", db.get("preact"), ob.preact, absx @ absw + np.abs(ob.b))
+    dp = np.abs(ob.d_prenorm).astype(np.float64)
+    check_sum_bound("dX", dx, dx_ref, dp @ absw.T)
+    # SGD with momentum 0: dv_w = (x^T . d_prenorm) / 512 / M
+    check_sum_bound("dv_w", db.get("dv_w"), ob.dv_w, (absx.T @ dp) / 512.0 / M)
 
 
 def test_c3_fp16_full_size(ctx):
@@ -104,6 +115,7 @@ def mlp_step(ctx, dims, M, hidden_kw, loss, loss_act, x, t, use_dropout, seeds):
     """FeedForwardNetwork::forward, compare, then FeedForwardNetwork::backward (ffn.rs:113-166:
     the layer above is updated before the layer below propagates through it)."""
     obs, dbs = build_net(ctx, dims, M, True, hidden_kw, seed=len(dims) * 100 + M)
+    w0 = [(ob.master_w.copy(), ob.master_norm_w.copy()) for ob in obs]   # before the step
     L = len(dims) - 1
     print(f"forward MLP {dims} x {M}", flush=True)
     cur_o, cur_d, outs = x, torch.from_numpy(x).cuda().half(), []
@@ -132,7 +144,24 @@ def mlp_step(ctx, dims, M, hidden_kw, loss, loss_act, x, t, use_dropout, seeds):
     for i in range(L - 2, -1, -1):
         dbs[i].backward_hidden(dbs[i + 1], dbs[i - 1].out if i > 0 else xd, tc, 1)
     torch.cuda.synchronize()
-    return obs, dbs
+    return obs, dbs, w0
+
+
+def check_layer_adam(i, ob, db, w0, norm):
+    """Every layer's optimiser state after the step: both moments and the master against
+    the oracle, and the master's update against Adam's closed form on the device's own
+    moments (master_w moves by ~1e-3 against |w| ~ 0.03-0.1, so its normwise check alone
+    could not see a wrong or sign-flipped update); the same for the norm weight."""
+    for n in ("dm_w", "dv_w", "master_w", "dm_b", "dv_b", "master_b"):
+        check(f"layer {i} {n}", db.get(n), getattr(ob, n), FP16_TOL)
+    check_adam_update(f"layer {i} master_w update", w0[0], db.get("master_w"), db.get("dm_w"), db.get("dv_w"), 1e-3,
+                      1, ob.master_w - w0[0], ob.dm_w)
+    if norm:
+        for n in ("dm_norm_w", "dv_norm_w", "master_norm_w"):
+            check(f"layer {i} {n}", db.get(n), getattr(ob, n), FP16_TOL)
+        check_adam_update(f"layer {i} master_norm_w update", w0[1], db.get("master_norm_w"), db.get("dm_norm_w"),
+                          db.get("dv_norm_w"), 1e-3, 1, ob.master_norm_w - w0[1], ob.dm_norm_w)
+    assert np.array_equal(db.get("w"), f16(db.get("master_w"))), f"layer {i}: W is not the RNE of its master"
 
 
 def test_c4_fp16_mlp_full_size(ctx):
@@ -143,11 +172,11 @@ def test_c4_fp16_mlp_full_size(ctx):
     t[np.arange(M), g.integers(0, 10, M)] = 1
     # weight ids of a fp16 training network built in order: 27 tensors per block (Q8)
     seeds = [O.scramble_seed(1, 27 * i) for i in range(len(dims) - 1)]
-    obs, dbs = mlp_step(ctx, dims, M, dict(norm=abi.NORM_RMS, act=abi.ACT_MISH, mask_coeff=0.1), abi.LOSS_CE,
-                        abi.ACT_SOFTMAX, x, t, True, seeds)
+    obs, dbs, w0 = mlp_step(ctx, dims, M, dict(norm=abi.NORM_RMS, act=abi.ACT_MISH, mask_coeff=0.1),
+                            abi.LOSS_CE, abi.ACT_SOFTMAX, x, t, True, seeds)
     for i, (ob, db) in enumerate(zip(obs, dbs)):
-        for n in ("d_prenorm", "dm_w", "master_w"):
-            check(f"layer {i} {n}", db.get(n), getattr(ob, n), FP16_TOL)
+        check(f"layer {i} d_prenorm", db.get("d_prenorm"), ob.d_prenorm, FP16_TOL)
+        check_layer_adam(i, ob, db, w0[i], i < len(obs) - 1)
 
 
 def test_c5_fp16_mlp_ragged_full_size(ctx):
@@ -155,8 +184,10 @@ def test_c5_fp16_mlp_ragged_full_size(ctx):
     g = rng(505)
     x = f16(g.standard_normal((M, 777)).astype(np.float32) * np.float32(np.sqrt(2.0)))   # variance 2
     t = (g.random((M, 13)) > 0.5).astype(np.float32)
-    obs, dbs = mlp_step(ctx, dims, M, dict(norm=abi.NORM_LAYER, act=abi.ACT_LEAKY, leaky=0.01), abi.LOSS_BCE,
-                        abi.ACT_SIGMOID, x, t, False, [0, 0, 0])
+    obs, dbs, w0 = mlp_step(ctx, dims, M, dict(norm=abi.NORM_LAYER, act=abi.ACT_LEAKY, leaky=0.01),
+                            abi.LOSS_BCE, abi.ACT_SIGMOID, x, t, False, [0, 0, 0])
     for i, (ob, db) in enumerate(zip(obs, dbs)):
-        for n in ("d_prenorm", "dm_w", "master_w", "dm_norm_w"):
-            check(f"layer {i} {n}", db.get(n), getattr(ob, n), FP16_TOL)
+        check(f"layer {i} d_prenorm", db.get("d_prenorm"), ob.d_prenorm, FP16_TOL)
+        check_layer_adam(i, ob, db, w0[i], i < len(obs) - 1)
+        if i < len(obs) - 1:
+            check(f"layer {i} dm_norm_b", db.get("dm_norm_b"), ob.dm_norm_b, FP16_TOL)

@@ -264,3 +264,38 @@ def test_kept_pad_input_grad_then_backward_bit_exact(ctx, monkeypatch):
             assert torch.equal(ta.view(bits), tb.view(bits)), f"step {step} {f} differs"
     del blocks
     ctx_ws.close()
+
+
+def test_kept_pad_stale_after_error_call_on_another_context(ctx):
+    """Context A's dW pads an odd-width block's d_prenorm_h and keeps the copy; an error
+    call on context B then rewrites that d_prenorm_h.  A's next GEMM on it, one call later
+    (the input gradient, which would take A's kept copy), must read the new values: its dx
+    equals, bit for bit, the one a context that never kept a copy computes."""
+    from soklyn_amd.devblock import DeviceBlock
+    M, K, N = 12345, 777, 1531   # C5's first layer: zero-padded operands, the dW keeps its copy
+    g = rng(707)
+    w = he_normal(g, K, N)
+    blk = DeviceBlock(ctx, K, N, M, w, half=True, master_w=w, act=abi.ACT_LEAKY, leaky=0.01)
+    stream = torch.cuda.current_stream().cuda_stream
+    ctx_b = abi.Context(0, 16, stream=stream)
+    ctx_c = abi.Context(0, 16, stream=stream)
+    try:
+        x = torch.from_numpy(f16(g.standard_normal((M, K)).astype(np.float32))).cuda().half()
+        s1, s2 = (torch.from_numpy((g.standard_normal((M, N)) * 512).astype(np.float32)).cuda() for _ in range(2))
+        blk.forward(x, M)
+        blk.error_from_sum(s1, M)
+        blk.backward(x, abi.train_ctx(abi.adam(), abi.adam(), M, 1e-3), 1)   # pads d_prenorm_h, keeps it
+        blk.ctx = ctx_b
+        blk.error_from_sum(s2, M)                                            # rewrites it on context B
+        blk.ctx = ctx
+        dx_a = blk.input_grad(M).cpu().numpy()
+        blk.ctx = ctx_c
+        dx_c = blk.input_grad(M).cpu().numpy()
+        blk.ctx = ctx
+        torch.cuda.synchronize()
+        assert np.array_equal(dx_a, dx_c), "context A read its stale padded copy of d_prenorm_h"
+        print(f"  dx after the rewrite on another context: bit-exact ({dx_a.size} elements)", flush=True)
+    finally:
+        torch.cuda.synchronize()
+        ctx_b.close()
+        ctx_c.close()

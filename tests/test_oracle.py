@@ -395,6 +395,39 @@ def test_hidden_error_and_input_grad_closed_form():
     assert rel(o1.input_grad(M), s) < 1e-5
 
 
+def test_hidden_error_and_input_grad_fp16_operands_rounded():
+    """backward_wmma.cu:44,51: in half mode the dX GEMM rounds both operands to f16 (d_prenorm and the
+    next layer's fp32 master W) and accumulates in f32.  Every operand is 0.45 fp16 ulp above an fp16
+    value in [1, 2), so each rounding moves it down by 0.45 ulp (2^-10): the oracle must agree with
+    float64 on the rounded operands to f32 summation noise, and disagree with the product of the
+    unrounded operands, or of either one unrounded, by far more than that."""
+    M, K0, N0, N1 = 20, 8, 48, 64
+    g = rng(31)
+
+    def off_grid(shape):
+        return (1.0 + (g.integers(0, 1000, shape) + 0.45) * 2.0 ** -10).astype(np.float32)
+
+    wm = off_grid((N0, N1))
+    o0 = O.OracleBlock(K0, N0, M, he_normal(g, K0, N0), half=True, act=0)
+    o1 = O.OracleBlock(N0, N1, M, O.round_f16(wm), half=True, act=0, master_w=wm)
+    s = off_grid((M, N1))
+    o1.error_from_sum(s, M)                   # identity, no norm: d_prenorm = s
+    assert np.array_equal(o1.d_prenorm, s)
+    dp64, w64 = s.astype(np.float64), wm.astype(np.float64)
+    rounded = O.round_f16(s).astype(np.float64) @ O.round_f16(wm).astype(np.float64).T
+    scale = np.abs(O.round_f16(s)).astype(np.float64) @ np.abs(O.round_f16(wm)).astype(np.float64).T
+    tol = 4 * N1 * 2.0 ** -24                  # sequential f32 accumulation of N1 terms
+    dx = o1.input_grad(M)
+    o0.hidden_error(o1, M)                    # identity: grad = mask * s = s
+    for name, got in (("input_grad", dx), ("hidden_error grad", o0.grad[:M])):
+        err = np.max(np.abs(got - rounded) / scale)
+        miss = np.max(np.abs(dp64 @ w64.T - rounded) / scale)
+        only_dp = np.max(np.abs(O.round_f16(s).astype(np.float64) @ w64.T - rounded) / scale)
+        only_w = np.max(np.abs(dp64 @ O.round_f16(wm).astype(np.float64).T - rounded) / scale)
+        assert err < tol, (name, err)
+        assert min(miss, only_dp, only_w) > 10 * tol, (name, miss, only_dp, only_w)
+
+
 # ---- optimisers --------------------------------------------------------------------------------------------
 def bwd_setup(seed, M=48, K=16, N=12, **kw):
     g = rng(seed)

@@ -1200,6 +1200,14 @@ static int32_t backward_impl(skl_ctx *ctx, const skl_dense_desc *b, const void *
     oe.regu_coeff = b->regularisation ? b->regu_coeff : 0.0f;
     oe.regularisation = b->regularisation;
     oe.ldc = N;
+    if (f16) {
+        // elements whose fp16-operand sum is not finite are summed again from these in fp32
+        oe.x = in;
+        oe.ldx = in_cols;
+        oe.dp32 = b->d_prenorm;
+        oe.lddp = N;
+        oe.batch = batch;
+    }
 
     // column partial sums for db / dNorm sums: left by the error call just
     // before, or made here in the workspace after the GEMM's region

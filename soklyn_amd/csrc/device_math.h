@@ -202,6 +202,17 @@ __device__ __forceinline__ NormGrad norm_grad(uint32_t norm, float e, float pren
     return g;
 }
 
+// dW of element (k, n) summed over the batch rows in fp32 from the fp32
+// d_prenorm, in the reference's order (backward.cu:181-186: sequential rows,
+// x converted to f32, one fused multiply-add per row).
+template <typename T>
+__device__ __attribute__((noinline)) float dw_element_f32(const T *x, uint32_t ldx, const float *dp, uint32_t lddp,
+                                                           uint32_t batch, uint32_t k, uint32_t n) {
+    float s = 0.0f;
+    for (uint32_t b = 0; b < batch; ++b) s = fmaf((float)x[(uint64_t)b * ldx + k], dp[(uint64_t)b * lddp + n], s);
+    return s;
+}
+
 // Optimiser hyper-parameters as the update kernels consume them
 // (backward.cu:105-154; bias corrections precomputed per call).
 struct OptParams {

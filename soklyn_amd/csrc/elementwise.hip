@@ -1450,7 +1450,8 @@ template <typename T, int VW> __global__ void __launch_bounds__(256) dw_reduce_o
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 float pj = p[j], vj = dv[j], mj = dm[j];
-                optimiser_step<sizeof(T) == 2>(pj, vj, mj, sum[j] * kLossScaleInv, e.inv_m, e.lr, e.clamp, e.opt,
+                const float gj = dw_checked<T>(e, r, c + j, sum[j]);
+                optimiser_step<sizeof(T) == 2>(pj, vj, mj, gj * kLossScaleInv, e.inv_m, e.lr, e.clamp, e.opt,
                                                e.regularisation, e.regu_coeff, true);
                 p[j] = pj;
                 dv[j] = vj;
@@ -1458,7 +1459,8 @@ template <typename T, int VW> __global__ void __launch_bounds__(256) dw_reduce_o
             }
             if (e.param) store4<T>(e.param, idx, p);
         } else {
-            optimiser_step<sizeof(T) == 2>(p, dv, dm, sum * kLossScaleInv, e.inv_m, e.lr, e.clamp, e.opt,
+            const float g = dw_checked<T>(e, r, c, sum);
+            optimiser_step<sizeof(T) == 2>(p, dv, dm, g * kLossScaleInv, e.inv_m, e.lr, e.clamp, e.opt,
                                            e.regularisation, e.regu_coeff, true);
             if (e.param) stv<T>(e.param, idx, from_f32<T>(p));
         }

@@ -243,13 +243,14 @@ template <typename T> struct EpiOptK {
         q.dv = *reinterpret_cast<const floatx4 *>(e.dv + idx);
         q.dm = *reinterpret_cast<const floatx4 *>(e.dm + idx);
     }
-    __device__ __forceinline__ static void finish(const OptEpi &e, uint64_t idx, uint32_t, uint32_t, floatx4 v,
+    __device__ __forceinline__ static void finish(const OptEpi &e, uint64_t idx, uint32_t m, uint32_t n, floatx4 v,
                                                   const Col &, const Pre &q) {
         floatx4 p = q.p, dv = q.dv, dm = q.dm;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             float pj = p[j], vj = dv[j], mj = dm[j];
-            optimiser_step<sizeof(T) == 2>(pj, vj, mj, v[j] * kLossScaleInv, e.inv_m, e.lr, e.clamp, e.opt,
+            const float g = dw_checked<T>(e, m, n + j, v[j]);
+            optimiser_step<sizeof(T) == 2>(pj, vj, mj, g * kLossScaleInv, e.inv_m, e.lr, e.clamp, e.opt,
                                            e.regularisation, e.regu_coeff, true);
             p[j] = pj; dv[j] = vj; dm[j] = mj;
         }
@@ -273,7 +274,8 @@ template <typename T> struct EpiOptK {
                                                   uint32_t) {
         const uint64_t idx = (uint64_t)m * e.ldc + n;
         float pj = e.master[idx], vj = e.dv[idx], mj = e.dm[idx];
-        optimiser_step<sizeof(T) == 2>(pj, vj, mj, v * kLossScaleInv, e.inv_m, e.lr, e.clamp, e.opt,
+        const float g = dw_checked<T>(e, m, n, v);
+        optimiser_step<sizeof(T) == 2>(pj, vj, mj, g * kLossScaleInv, e.inv_m, e.lr, e.clamp, e.opt,
                                        e.regularisation, e.regu_coeff, true);
         e.master[idx] = pj;
         e.dv[idx] = vj;
@@ -295,7 +297,8 @@ template <typename T> struct EpiOptK {
                 if (c >= sh.N) break;
                 const uint64_t idx = base + c;
                 float pj = e.master[idx], vj = e.dv[idx], mj = e.dm[idx];
-                optimiser_step<sizeof(T) == 2>(pj, vj, mj, v[j] * kLossScaleInv, e.inv_m, e.lr, e.clamp, e.opt,
+                const float g = dw_checked<T>(e, m, c, v[j]);
+                optimiser_step<sizeof(T) == 2>(pj, vj, mj, g * kLossScaleInv, e.inv_m, e.lr, e.clamp, e.opt,
                                                e.regularisation, e.regu_coeff, true);
                 e.master[idx] = pj;
                 e.dv[idx] = vj;

@@ -48,6 +48,13 @@ struct OptEpi {
     // blocks w, w + grid, ... < vec_blocks of the bias / norm-parameter update
     uint32_t vec_blocks;
     VecOptArgs vec;
+    // fp16 blocks: an element whose sum over fp16 operands is not finite (a
+    // d_prenorm beyond the fp16 range made its fp16 copy infinite) is summed
+    // again in fp32 from these, as the reference's fp32 dW does
+    // (backward.cu:181-186); null dp32: no such check
+    const void *x;           // the dW's input rows [batch x K] at pitch ldx, T
+    const float *dp32;       // d_prenorm [batch x N] at pitch lddp
+    uint32_t ldx, lddp, batch, pad2;
 };
 
 // Plain fp32 store (input gradient) or split-K partial store.

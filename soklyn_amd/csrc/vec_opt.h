@@ -8,6 +8,16 @@
 
 namespace skl {
 
+// The gradient sum of W element (k, n): the sum over fp16 operands, or, where
+// that is not finite on an fp16 block, the fp32 sum (OptEpi::dp32).
+template <typename T> __device__ __forceinline__ float dw_checked(const OptEpi &e, uint32_t k, uint32_t n, float v) {
+    if constexpr (sizeof(T) == 2) {
+        if (__builtin_expect(!__builtin_isfinite(v), 0) && e.dp32)
+            return dw_element_f32<T>(reinterpret_cast<const T *>(e.x), e.ldx, e.dp32, e.lddp, e.batch, k, n);
+    }
+    return v;
+}
+
 // a.cpb columns per workgroup (a power of 2), NT / cpb lanes per column: lane j
 // sums the partials of splits j, j + lanes, ... in order (8 loads in flight), then
 // the lanes of a column are added in a fixed tree (halving strides).  cpb comes

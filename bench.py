@@ -82,6 +82,9 @@ def parse():
     p.add_argument("--config", default="c3", choices=sorted(CONFIGS))
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-rows", type=int, default=0, help="rows of the CPU baseline sample (0 = auto)")
+    p.add_argument("--power-ms", type=float, default=2000.0,
+                   help="after the timed steps, run the step untimed this long while amd-smi samples the "
+                        "socket power and graphics clock (0 = skip)")
     p.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                    help="only run a plain device-to-device copy of MIB MiB (counter calibration) and exit")
     return p.parse_args()
@@ -160,6 +163,54 @@ def host_cpu():
     except OSError:
         pass
     return {"cpu_model": model, "host_cores_available": len(os.sched_getaffinity(0))}
+
+
+def _smi_sample(gpu: int = 0):
+    """One `amd-smi metric -p -c` reading of GPU `gpu`: (socket power W, mean graphics clock MHz
+    over the XCDs), or None when the tool or a field is unavailable."""
+    import re
+    import subprocess
+    try:
+        out = subprocess.run(["amd-smi", "metric", "-g", str(gpu), "-p", "-c"], capture_output=True,
+                             text=True, timeout=5).stdout
+    except (OSError, subprocess.SubprocessError):
+        return None
+    p = re.search(r"SOCKET_POWER: (\d+(?:\.\d+)?) W", out)
+    clks = [float(c) for c in re.findall(r"GFX_\d+:\s*\n\s*CLK: (\d+(?:\.\d+)?) MHz", out)]
+    if not p or not clks:
+        return None
+    return float(p.group(1)), sum(clks) / len(clks)
+
+
+def power_pass(step, ms: float, sync):
+    """Run `step` untimed for `ms` of wall time while a thread samples amd-smi; returns the mean
+    socket power and graphics clock over the samples after the first 0.5 s (the tool's power
+    reading is a running average that lags the load), or None."""
+    import threading
+    samples, stop = [], threading.Event()
+    t0 = time.perf_counter()
+
+    def sampler():
+        while not stop.is_set():
+            r = _smi_sample()
+            if r is None:
+                return
+            samples.append((time.perf_counter() - t0, *r))
+
+    th = threading.Thread(target=sampler, daemon=True)
+    th.start()
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(4):
+            step()
+        sync()
+    stop.set()
+    th.join(timeout=10)
+    kept = [s for s in samples if s[0] >= 0.5]
+    if not kept:
+        return None
+    return {"socket_w": round(sum(s[1] for s in kept) / len(kept), 1),
+            "gfx_mhz": round(sum(s[2] for s in kept) / len(kept), 1), "samples": len(kept),
+            "source": "amd-smi metric -p -c during an untimed pass of the same step after the timed ones"}
 
 
 def cpu_baseline_block(cfg, rows: int, reps: int = 3):
@@ -404,6 +455,9 @@ def main():
                 for i, c in enumerate(names)}
     call_ms = avg(evs, calls)     # each hot-path call in the step
     kern = avg(gevs, gemms)       # the GEMM kernels alone
+    # Socket power and graphics clock under this step (the GEMMs run at the board's power
+    # limit, where the clock settles well below the 2.4 GHz of the published peak)
+    power = power_pass(bench.step, args.power_ms, torch.cuda.synchronize) if args.power_ms > 0 else None
 
     # The roofline kernel: the slowest of the timed GEMM kernels
     dom = max(gemms, key=lambda k: kern[k])
@@ -442,6 +496,12 @@ def main():
                      "kernel_ms": {k: round(v, 4) for k, v in kern.items()},
                      "call_ms": {k: round(v, 4) for k, v in call_ms.items()}},
     }
+    if power is not None:
+        # the dense fp16 / fp32 MFMA peak at the measured clock, for reading the roofline
+        # fraction against the clock the power limit leaves
+        power["peak_at_clock"] = round(peak * power["gfx_mhz"] / 2400.0, 1)
+        power["kernel_frac_at_clock"] = round(achieved / power["peak_at_clock"], 4)
+    out["power"] = power
     # bandwidth-bound calls made of one element-wise kernel: algorithmic bytes / call time
     if bench.hbm_bytes:
         out["hbm_kernels"] = {

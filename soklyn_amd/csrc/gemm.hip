@@ -588,13 +588,14 @@ bool gemm_direct_ok(const GemmLaunch &g) {
            (g.splits == 0 || g.splits == 1);
 }
 
-// 256x256: 8 waves per workgroup for every layout (two per SIMD: one issues
-// MFMAs while the other waits on LDS; see gemm_dma.h); the MFMA shape per
-// layout: v_mfma_f32_16x16x32_f16 when A is k-contiguous (C3 shapes: dX 2%
-// faster back to back, 5% with a cold last-level cache; forward 2-3%);
-// 32x32x16 when both operands are transposed (dW), whose 16x16 fragments at 8
-// waves overflow the register budget even with A single-buffered.  128x128:
-// 4 waves of 64x64, two workgroups per CU, 16x16x32 for every layout.
+// 256x256: 4 waves (one per SIMD, 16x16x32 MFMAs on AGPR accumulators) for the
+// epilogues DmaOneWave selects on whole tiles; otherwise 8 waves (two per SIMD: one
+// issues MFMAs while the other waits on LDS; see gemm_dma.h) with
+// v_mfma_f32_16x16x32_f16 when A is k-contiguous (C3 shapes: dX 2% faster back to
+// back, 5% with a cold last-level cache; forward 2-3%) and 32x32x16 when both
+// operands are transposed, whose 16x16 fragments at 8 waves overflow the register
+// budget even with A single-buffered.  128x128: 4 waves of 64x64, two workgroups per
+// CU, 16x16x32 for every layout.
 template <class Epi, bool AK, bool BK_, int NW, int MI, int BT>
 static hipError_t run_dma_t(const GemmLaunch &g, const typename Epi::Params &p, uint32_t splits, uint32_t kps,
                             hipStream_t s) {
@@ -615,17 +616,30 @@ static hipError_t run_dma_t(const GemmLaunch &g, const typename Epi::Params &p, 
     const half_t *B = reinterpret_cast<const half_t *>(g.B);
     if (dma_full_epilogue(g))
         launch_timed(g, gemm_dma_kernel<Epi, AK, BK_, NW, false, MI, BT>, grid, dim3(64 * NW), s, sh, A, B, p);
-    else if constexpr (EpiSums<Epi>::value)
-        return hipErrorInvalidValue;   // whole tiles only (hidden_err_fusable)
+    else if constexpr (EpiSums<Epi>::value || (NW == 4 && BT == 256))
+        return hipErrorInvalidValue;   // whole tiles only (hidden_err_fusable; the one-wave-per-SIMD tile)
     else
         launch_timed(g, gemm_dma_kernel<Epi, AK, BK_, NW, true, MI, BT>, grid, dim3(64 * NW), s, sh, A, B, p);
     return hipGetLastError();
 }
 
+// Epilogues that run the 256x256 tile with one wave per SIMD (4 waves, 16x16x32 MFMAs
+// on AGPR accumulators, a third fewer LDS fragment bytes per flop than 8 waves): the
+// fp32 store (dX, split-K dW partials) and the fused optimiser.  Measured on the C3
+// shapes against 8 waves on one box: main loop 4% faster per k for dX and dW; dX
+// 213.1 -> 207.7 us, dW + Adam 281.3 -> 267.8 us.  The forward and the fused hidden
+// error keep 8 waves: their store-heavy epilogues run slower with half the threads
+// (forward 225.0 -> 241.3 us).
+template <class Epi> struct DmaOneWave { static constexpr bool value = false; };
+template <> struct DmaOneWave<EpiStoreK> { static constexpr bool value = true; };
+template <> struct DmaOneWave<EpiOptK<half_t>> { static constexpr bool value = true; };
+
 template <class Epi, bool AK, bool BK_>
 static hipError_t run_dma(const GemmLaunch &g, const typename Epi::Params &p, uint32_t splits, uint32_t kps,
                           hipStream_t s) {
     if (g.tile == 128) return run_dma_t<Epi, AK, BK_, 4, 16, 128>(g, p, splits, kps, s);
+    if constexpr (DmaOneWave<Epi>::value)
+        if (dma_full_epilogue(g)) return run_dma_t<Epi, AK, BK_, 4, 16, 256>(g, p, splits, kps, s);
     return run_dma_t<Epi, AK, BK_, 8, AK ? 16 : 32, 256>(g, p, splits, kps, s);
 }
 

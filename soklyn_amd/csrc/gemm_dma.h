@@ -11,16 +11,19 @@
 //    fragments are single-buffered (fragment i of the next k-step is read in
 //    place after its row's MFMAs), which keeps 8 waves inside the register
 //    budget when A is k-contiguous.
-//  * NW = 4 or 8 waves.  NW = 4: one wave per SIMD, wave tile 128 x 128 =
-//    4 x 4 v_mfma_f32_32x32x16_f16 blocks, 256 accumulators per lane in AGPRs;
-//    per k-step a wave reads 8 x 1 KB fragments for 16 MFMAs.  NW = 8: two
-//    waves per SIMD, wave tile 128 x 64 (4 x 2 blocks, 128 accumulators), 1.5x
-//    the LDS fragment bytes per flop, but while one wave of a SIMD waits on its
-//    LDS reads the other issues MFMAs.  Measured on the C3 shapes (random fp16
-//    data, 30 launches back to back): 8 waves run the layouts with a
-//    transposing (m/n-contiguous) operand 6-7% faster and, with the
-//    interleaved schedule below, the all-k-contiguous layout 2% faster, so the
-//    launcher uses 8.
+//  * NW = 4 or 8 waves.  NW = 4 on a 256 x 256 tile: one wave per SIMD, wave
+//    tile 128 x 128 = 8 x 8 v_mfma_f32_16x16x32_f16 blocks, 256 accumulators per
+//    lane held in AGPRs by an asm MFMA (DmaMma<16>::run_agpr), both fragment sets
+//    double-buffered, 16 fragment reads and 16 DMA instructions spread evenly over
+//    the 64 MFMAs of a k-step.  NW = 8: two waves per SIMD, wave tile 128 x 64
+//    (128 accumulators), 1.5x the LDS fragment bytes per flop, but while one wave
+//    of a SIMD waits on its LDS reads the other issues MFMAs.  The GEMMs run at the
+//    board's power limit (the clock settles near 1.8-2.0 GHz), where fewer bytes
+//    per flop buy clock: on the C3 shapes the 4-wave main loop is ~4% faster per k
+//    than the 8-wave one for every layout, but with half the threads the
+//    store-heavy epilogues (forward caches, fused hidden error) run slower, so the
+//    launcher takes 4 waves for the fp32-store and optimiser epilogues and 8 for
+//    the others.
 //  * BK = 64 halves; 2 stages of 64 KB (A tile + B tile, 32 KB each, laid out
 //    per operand layout as described at OpK / OpN).  Stages are filled by
 //    buffer_load_dwordx4 ... lds (no staging registers, no ds_write): one wave
@@ -96,6 +99,15 @@ template <> struct DmaMma<16> {
     __device__ __forceinline__ static void run(Acc &acc, const u32x4 &bop, const u32x4 &aop) {
         acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(halfx8, bop), __builtin_bit_cast(halfx8, aop),
                                                      acc, 0, 0, 0);
+    }
+    // The same MFMA with the accumulator bound to AGPRs by the asm constraint.  With
+    // 256 accumulators per lane (one wave per SIMD) the register allocator, left to
+    // itself, moves them between AGPRs and VGPRs around the k loop and spills.  The
+    // compiler's hazard checks do not see into the asm: the kernel adds the wait
+    // states itself (after zeroing the accumulators, before the epilogue reads them);
+    // inside the loop no VALU writes a VGPR or AGPR these MFMAs read.
+    __device__ __forceinline__ static void run_agpr(Acc &acc, const u32x4 &bop, const u32x4 &aop) {
+        asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(bop), "v"(aop));
     }
 };
 
@@ -379,6 +391,17 @@ __global__ void __launch_bounds__(64 * NW)
         for (int j = 0; j < C::NTL; ++j)
 #pragma unroll
             for (int r = 0; r < (int)(sizeof(typename MM::Acc) / 4); ++r) acc[i][j][r] = 0.0f;
+    // one wave per SIMD on a 256 x 256 tile: 16x16x32 MFMAs on AGPR accumulators
+    // (DmaMma<16>::run_agpr), both fragment sets double-buffered, reads and DMA spread
+    // evenly over each k-step
+    constexpr bool AGPR_ASM = MI == 16 && NW == 4 && BT == 256;
+    if constexpr (AGPR_ASM) {
+        // two wait states between each accumulator's zeroing and its first MFMA
+#pragma unroll
+        for (int i = 0; i < C::MT; ++i)
+#pragma unroll
+            for (int j = 0; j < C::NTL; ++j) asm volatile("s_nop 1" : "+a"(acc[i][j]));
+    }
 
     typename OA::Frag fa[2];
     typename OB::Frag fb[2];
@@ -399,8 +422,15 @@ __global__ void __launch_bounds__(64 * NW)
     };
     auto mfma = [&](int set, int q) {
         const int i = q / C::NTL, j = q % C::NTL;
-        MM::run(acc[i][j], OB::op(fb[set], j), OA::op(fa[set], i));
+        if constexpr (AGPR_ASM)
+            DmaMma<16>::run_agpr(acc[i][j], OB::op(fb[set], j), OA::op(fa[set], i));
+        else
+            MM::run(acc[i][j], OB::op(fb[set], j), OA::op(fa[set], i));
     };
+    // one wave per SIMD: fragment f of the next k-step behind MFMA f * RSP, the k-step's
+    // DMA instruction d behind MFMA d * DSP + 1 (a burst of reads behind the first MFMAs
+    // stalled the lone wave: main loop 3-4% slower on the C3 shapes)
+    constexpr int RSP = NMM / NFR > 0 ? NMM / NFR : 1, DSP = NMM / NDMA > 0 ? NMM / NDMA : 1;
     auto dma = [&](int kt, int stage, int q) {
         lds_char *st = lsm + stage * C::STAGEB + wave * 1024u;
         if (q < OA::IPO)
@@ -425,15 +455,19 @@ __global__ void __launch_bounds__(64 * NW)
 #pragma unroll
         for (int q = 0; q < NMM; ++q) {
             mfma(cur, q);
+            if constexpr (AGPR_ASM) {
+                if (q % RSP == 0 && q / RSP < NFR) read_frag(cur ^ 1, stage, ks_next, q / RSP);
+            } else {
 #pragma unroll
-            for (int u = 0; u < FPM; ++u)
-                if (q * FPM + u < NFR) read_frag(cur ^ 1, stage, ks_next, q * FPM + u);
+                for (int u = 0; u < FPM; ++u)
+                    if (q * FPM + u < NFR) read_frag(cur ^ 1, stage, ks_next, q * FPM + u);
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
     };
 
     const int klast = kb + nk - 1;
-    if constexpr (MI == 16) {
+    if constexpr (MI == 16 && !AGPR_ASM) {
         // 16x16x32: A fragments single-buffered, B double-buffered.  A fragment i
         // of the next k-step is read in place right after row i's MFMAs (its last
         // use), the next k-step's B fragments behind row 0's MFMAs.  LDS reads
@@ -535,10 +569,15 @@ __global__ void __launch_bounds__(64 * NW)
 #pragma unroll
             for (int q = 0; q < NMM; ++q) {
                 mfma(1, q);
-                if (q < NDMA) dma(kn, s, q);
+                if constexpr (AGPR_ASM) {
+                    if (q % DSP == 1 % DSP && q / DSP < NDMA) dma(kn, s, q / DSP);
+                    if (q % RSP == 0 && q / RSP < NFR) read_frag(0, s ^ 1, 0, q / RSP);
+                } else {
+                    if (q < NDMA) dma(kn, s, q);
 #pragma unroll
-                for (int u = 0; u < FPM; ++u)
-                    if (q * FPM + u < NFR) read_frag(0, s ^ 1, 0, q * FPM + u);
+                    for (int u = 0; u < FPM; ++u)
+                        if (q * FPM + u < NFR) read_frag(0, s ^ 1, 0, q * FPM + u);
+                }
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
@@ -546,6 +585,15 @@ __global__ void __launch_bounds__(64 * NW)
     }
     wait_vmcnt<0>();     // no DMA may land in the epilogue's staging area
     wait_lgkmcnt<0>();
+    if constexpr (AGPR_ASM) {
+        // wait states before the epilogue's reads of the last MFMAs' accumulators (the
+        // empty statements that claim to rewrite each accumulator keep those reads below)
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+#pragma unroll
+        for (int i = 0; i < C::MT; ++i)
+#pragma unroll
+            for (int j = 0; j < C::NTL; ++j) asm volatile("" : "+a"(acc[i][j]));
+    }
     __syncthreads();
 
     // Epilogue through LDS: passes of 128 rows (rows of accumulator block

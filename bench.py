@@ -22,6 +22,11 @@ wall time (default 250): under load the GPU's clocks take ~50 ms to reach their
 steady state, and with few warm-up steps the timed steps would fall in that
 ramp (C3: 855 TFLOP/s with 5 warm-up steps, 885-930 once settled).  The timed
 region is still exactly K steps; the line reports the settle time and steps.
+Inside the timed steps only the roofline GEMM kernel (the step's slowest GEMM,
+named per configuration) carries HIP events, recorded by its own dispatch; every
+GEMM kernel and every call is timed again in an untimed pass after them
+(`kernel_ms`, `call_ms`).  Then, unless --power-ms 0, the step runs untimed while
+amd-smi samples the socket power and graphics clock (`power`).
 Prints one JSON line.
 """
 from __future__ import annotations
@@ -47,11 +52,11 @@ LOSS_CE, LOSS_BCE = 1, 2
 
 CONFIGS = {
     # BASELINE.json configs[2] (headline) and configs[1]: single DenseBlocks
-    "c3": dict(kind="block", M=8192, K=4096, N=4096, half=True, act=ACT_SILU,
+    "c3": dict(kind="block", M=8192, K=4096, N=4096, half=True, act=ACT_SILU, roof="dw_gemm",
                metric=HEADLINE,
                workload="DenseBlock fp16 mixed precision, X[8192x4096] f16, W[4096x4096] f16 copy of fp32 "
                         "He-normal master, SiLU, fwd+bwd(dX,dW)+Adam"),
-    "c2": dict(kind="block", M=4096, K=1024, N=1024, half=False, act=ACT_RELU,
+    "c2": dict(kind="block", M=4096, K=1024, N=1024, half=False, act=ACT_RELU, roof="forward_gemm",
                metric="DenseBlock fwd+bwd TFLOP/s & % MFMA peak (fp32, B=4096, 1024→1024)",
                workload="DenseBlock fp32, X[4096x1024], W[1024x1024] He-normal, ReLU, fwd+bwd(dX,dW,db)+SGD"),
     # multi-layer train steps
@@ -316,6 +321,7 @@ class BlockBench:
         self.step_no = 0
         self.flops = 3 * 2.0 * M * K * N
         self.kernel_flops = {g: 2.0 * M * K * N for g in self.gemms}
+        self.roof = cfg["roof"]   # the slowest GEMM of the step (checked against the untimed pass)
         self.stream, self.ctx = stream, ctx
         # error_from_sum is one element-wise kernel: its algorithmic HBM bytes (the
         # activation derivative reads predrop for sigmoid / ReLU / leaky ReLU / tanh /
@@ -328,15 +334,15 @@ class BlockBench:
 
     def step(self, ev=None, gev=None):
         # ev: per-call (start, end) HIP events on the launch stream (a diagnostic pass
-        # after the timed steps); gev: events the library records around the GEMM
-        # kernel alone of the forward and dX calls (inside the timed steps)
+        # after the timed steps); gev: {GEMM name: (start, end)} events the library records
+        # around that GEMM kernel alone, carried by its dispatch
         self.step_no += 1
         b, M = self.blk, self.M
         fns = (lambda: b.forward(self.x, M), lambda: b.error_from_sum(self.dy, M),
                lambda: b.input_grad(M, self.dx), lambda: b.backward(self.x, self.tc, self.step_no))
-        gemm_of = {0: 0, 2: 2, 3: 1}   # call index -> index in self.gemms
+        gemm_of = {0: "forward_gemm", 2: "dx_gemm", 3: "dw_gemm"}   # call index -> GEMM name
         for i, fn in enumerate(fns):
-            if gev is not None and i in gemm_of:
+            if gev is not None and gemm_of.get(i) in gev:
                 self.ctx.time_next_gemm(*gev[gemm_of[i]])
             if ev is not None:
                 ev[i][0].record(self.stream)
@@ -374,6 +380,7 @@ class MlpBench:
         self.timed = f"hidden_error_gemm_layer{k}"
         self.calls = (f"backward_hidden_layer{k}",)
         self.gemms = (self.timed,)
+        self.roof = self.timed
         self.kernel_flops = {self.timed: 2.0 * M * dims[k + 1] * dims[k + 2]}
         self.hbm_bytes = {}
         self.ctx = ctx
@@ -390,7 +397,7 @@ class MlpBench:
         for i in range(L - 2, -1, -1):
             timed = i == cfg["timed_layer"]
             if timed and gev is not None:
-                self.ctx.time_next_gemm(*gev[0])
+                self.ctx.time_next_gemm(*gev[self.timed])
             if timed and ev is not None:
                 ev[0][0].record(self.stream)
             # gpu_hidden_layer_backward_pass (ffn.rs:156 -> mlp.rs:728): hidden error, then dW
@@ -421,9 +428,13 @@ def main():
     bench = BlockBench(cfg, ctx, stream) if cfg["kind"] == "block" else MlpBench(cfg, ctx, stream)
     calls, gemms = bench.calls, bench.gemms
 
-    # events first, so nothing but the warm-up steps runs between warm-up and timing
+    # events first, so nothing but the warm-up steps runs between warm-up and timing.
+    # In the timed steps only the roofline GEMM kernel carries events: each kernel-carried
+    # pair leaves the GPU idle for ~5 us around its kernel (three pairs cost a C3 step
+    # 1.8%); every GEMM is timed in the untimed pass after them.
     evs = [timing_events(len(calls)) for _ in range(args.steps)]
-    gevs = [timing_events(len(gemms)) for _ in range(args.steps)]
+    gevs = [dict(zip(gemms, timing_events(len(gemms)))) for _ in range(args.steps)]
+    rev = [{bench.roof: timing_events(1)[0]} for _ in range(args.steps)]
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     settle_steps, t_settle = 0, time.perf_counter()
@@ -438,30 +449,34 @@ def main():
     t0 = time.perf_counter()
     ev0.record(stream)
     for k in range(args.steps):
-        bench.step(None, gevs[k])     # only the roofline GEMM kernels carry events
+        bench.step(None, rev[k])      # only the roofline GEMM kernel carries events
     ev1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms = ev0.elapsed_time(ev1) / args.steps
     value = bench.flops / (ms * 1e-3) / 1e12
-    # Per-call times come from a second, untimed pass: recorded inside the timed
-    # steps, the 8 extra events of a C3 step cost ~3.5% of its time.
+    # Per-call and per-GEMM times come from a second, untimed pass: recorded inside the
+    # timed steps, the 8 extra events of a C3 step cost ~3.5% of its time.
     for k in range(args.steps):
-        bench.step(evs[k], None)
+        bench.step(evs[k], gevs[k])
     torch.cuda.synchronize()
 
     def avg(table, names):
         return {c: sum(table[k][i][0].elapsed_time(table[k][i][1]) for k in range(args.steps)) / args.steps
                 for i, c in enumerate(names)}
     call_ms = avg(evs, calls)     # each hot-path call in the step
-    kern = avg(gevs, gemms)       # the GEMM kernels alone
+    kern = {g: sum(gevs[k][g][0].elapsed_time(gevs[k][g][1]) for k in range(args.steps)) / args.steps
+            for g in gemms}       # the GEMM kernels alone (untimed pass)
+    roof_ms = sum(rev[k][bench.roof][0].elapsed_time(rev[k][bench.roof][1])
+                  for k in range(args.steps)) / args.steps   # the roofline kernel in the timed steps
     # Socket power and graphics clock under this step (the GEMMs run at the board's power
     # limit, where the clock settles well below the 2.4 GHz of the published peak)
     power = power_pass(bench.step, args.power_ms, torch.cuda.synchronize) if args.power_ms > 0 else None
 
-    # The roofline kernel: the slowest of the timed GEMM kernels
-    dom = max(gemms, key=lambda k: kern[k])
-    achieved = bench.kernel_flops[dom] / (kern[dom] * 1e-3) / 1e12
+    # The roofline kernel: the step's slowest GEMM, timed inside the timed steps
+    dom = bench.roof
+    slowest = max(gemms, key=lambda k: kern[k])
+    achieved = bench.kernel_flops[dom] / (roof_ms * 1e-3) / 1e12
     half = cfg.get("half", True)
     peak = PEAK["f16" if half else "f32"]
     trec = traffic_record(args.config, dom)
@@ -493,6 +508,7 @@ def main():
                      "frac": round(achieved / peak, 4),
                      "traffic": trec["bytes_per_launch"] if trec else None,
                      "traffic_source": trec["source"] if trec else None, "kernel": dom,
+                     "kernel_ms_timed": round(roof_ms, 4), "slowest_gemm_untimed_pass": slowest,
                      "kernel_ms": {k: round(v, 4) for k, v in kern.items()},
                      "call_ms": {k: round(v, 4) for k, v in call_ms.items()}},
     }

@@ -209,6 +209,12 @@ struct EpiStoreK {
                                                   const Col &, const Pre &) {
         __builtin_nontemporal_store(v, reinterpret_cast<floatx4 *>(e.out + idx));
     }
+    // one-wave-per-SIMD tiles: from the accumulator registers (half-line row segments,
+    // so a plain store the L2 can join)
+    static constexpr bool kDirect = true;
+    __device__ __forceinline__ static void direct(const StoreEpi &e, uint64_t idx, floatx4 v) {
+        *reinterpret_cast<floatx4 *>(e.out + idx) = v;
+    }
     struct Col1 {};
     __device__ __forceinline__ static Col1 column1(const StoreEpi &, uint32_t) { return Col1{}; }
     __device__ __forceinline__ static void apply1(const StoreEpi &e, uint32_t m, uint32_t n, float v, const Col1 &,

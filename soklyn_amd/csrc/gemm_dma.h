@@ -311,6 +311,12 @@ template <class E> struct EpiSums<E, std::void_t<decltype(E::kColSums)>> {
 template <class E, class = void> struct EpiVec8 { static constexpr bool value = false; };
 template <class E> struct EpiVec8<E, std::void_t<decltype(E::kVec)>> { static constexpr bool value = E::kVec == 8; };
 
+// Epilogues with kDirect store each accumulator block from its registers
+// (direct(params, idx, 4 columns)) when the tile runs one wave per SIMD on whole
+// tiles, instead of going through LDS.
+template <class E, class = void> struct EpiDirect { static constexpr bool value = false; };
+template <class E> struct EpiDirect<E, std::void_t<decltype(E::kDirect)>> { static constexpr bool value = E::kDirect; };
+
 // MFMAs per DMA instruction in a tile's last k-step, where the refill of the
 // stage just read is issued (16x16x32 schedule): 1 = all of them behind the
 // first MFMAs.  Measured on C3 / C4 (steady clocks): every second MFMA runs the
@@ -593,6 +599,21 @@ __global__ void __launch_bounds__(64 * NW)
         for (int i = 0; i < C::MT; ++i)
 #pragma unroll
             for (int j = 0; j < C::NTL; ++j) asm volatile("" : "+a"(acc[i][j]));
+    }
+    if constexpr (AGPR_ASM && EpiDirect<Epi>::value && !EDGE) {
+        // a lane's accumulator block holds 4 consecutive columns of one row: stored
+        // straight from the AGPRs, each instruction 16 rows x 64 bytes (the L2 joins
+        // the two halves of each line), no LDS round trip (C3 dX 210.4 -> 204.2 us in
+        // the step)
+        const typename Epi::Params eps = Epi::at_split(ep, blockIdx.y);
+#pragma unroll
+        for (int i = 0; i < C::MT; ++i) {
+            const uint32_t m = m0 + wm * C::TWM + i * MI + (lane & 15u);
+#pragma unroll
+            for (int j = 0; j < C::NTL; ++j)
+                Epi::direct(eps, (uint64_t)m * Epi::ldc(eps) + n0 + wn * C::TWN + j * MI + (lane >> 4) * 4u, acc[i][j]);
+        }
+        return;
     }
     __syncthreads();
 

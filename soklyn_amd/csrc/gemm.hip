@@ -212,7 +212,9 @@ struct EpiStoreK {
     // one-wave-per-SIMD tiles: from the accumulator registers (half-line row segments,
     // so a plain store the L2 can join)
     static constexpr bool kDirect = true;
-    __device__ __forceinline__ static void direct(const StoreEpi &e, uint64_t idx, floatx4 v) {
+    static constexpr int kDirectBatch = 8;
+    __device__ __forceinline__ static void direct(const StoreEpi &e, uint64_t idx, uint32_t, uint32_t, floatx4 v,
+                                                  const Pre &) {
         *reinterpret_cast<floatx4 *>(e.out + idx) = v;
     }
     struct Col1 {};

@@ -311,11 +311,21 @@ template <class E> struct EpiSums<E, std::void_t<decltype(E::kColSums)>> {
 template <class E, class = void> struct EpiVec8 { static constexpr bool value = false; };
 template <class E> struct EpiVec8<E, std::void_t<decltype(E::kVec)>> { static constexpr bool value = E::kVec == 8; };
 
-// Epilogues with kDirect store each accumulator block from its registers
-// (direct(params, idx, 4 columns)) when the tile runs one wave per SIMD on whole
-// tiles, instead of going through LDS.
-template <class E, class = void> struct EpiDirect { static constexpr bool value = false; };
-template <class E> struct EpiDirect<E, std::void_t<decltype(E::kDirect)>> { static constexpr bool value = E::kDirect; };
+// Epilogues with kDirect finish each accumulator block from its registers
+// (direct(params, idx, m, n, 4 columns, its loads)) when the tile runs one wave per
+// SIMD on whole tiles, instead of going through LDS; the per-element loads of
+// kDirectBatch blocks are issued before any of them is used.  Only stores take it:
+// loads in this shape (16 rows x 64 bytes per instruction, rows a power-of-two
+// pitch apart) ran the fused optimiser's epilogue ~10x slower (C3 dW + Adam
+// 272 -> 3090 us), the rows falling into few vector-L1 sets.
+template <class E, class = void> struct EpiDirect {
+    static constexpr bool value = false;
+    static constexpr int batch = 1;
+};
+template <class E> struct EpiDirect<E, std::void_t<decltype(E::kDirect)>> {
+    static constexpr bool value = E::kDirect;
+    static constexpr int batch = E::kDirectBatch;
+};
 
 // MFMAs per DMA instruction in a tile's last k-step, where the refill of the
 // stage just read is issued (16x16x32 schedule): 1 = all of them behind the
@@ -605,13 +615,29 @@ __global__ void __launch_bounds__(64 * NW)
         // straight from the AGPRs, each instruction 16 rows x 64 bytes (the L2 joins
         // the two halves of each line), no LDS round trip (C3 dX 210.4 -> 204.2 us in
         // the step)
+        // (the kernel ends here: an epilogue with work after its tiles, the fused
+        // optimiser's bias update, must not take this path)
+        static_assert(!std::is_same<typename Epi::Params, OptEpi>::value, "direct epilogue with a trailing update");
         const typename Epi::Params eps = Epi::at_split(ep, blockIdx.y);
+        constexpr int DB = EpiDirect<Epi>::batch;   // blocks whose per-element loads go first
+        static_assert(C::NTL % DB == 0, "direct epilogue batch");
 #pragma unroll
         for (int i = 0; i < C::MT; ++i) {
             const uint32_t m = m0 + wm * C::TWM + i * MI + (lane & 15u);
 #pragma unroll
-            for (int j = 0; j < C::NTL; ++j)
-                Epi::direct(eps, (uint64_t)m * Epi::ldc(eps) + n0 + wn * C::TWN + j * MI + (lane >> 4) * 4u, acc[i][j]);
+            for (int jb = 0; jb < C::NTL; jb += DB) {
+                typename Epi::Pre pre[DB];
+#pragma unroll
+                for (int u = 0; u < DB; ++u) {
+                    const uint32_t n = n0 + wn * C::TWN + (jb + u) * MI + (lane >> 4) * 4u;
+                    Epi::load(eps, (uint64_t)m * Epi::ldc(eps) + n, m, pre[u]);
+                }
+#pragma unroll
+                for (int u = 0; u < DB; ++u) {
+                    const uint32_t n = n0 + wn * C::TWN + (jb + u) * MI + (lane >> 4) * 4u;
+                    Epi::direct(eps, (uint64_t)m * Epi::ldc(eps) + n, m, n, acc[i][jb + u], pre[u]);
+                }
+            }
         }
         return;
     }

@@ -13,8 +13,13 @@ checks, for every such kernel, the invariants those wait states rely on:
     states later (an XDL write followed by a VALU or memory read needs up to 19 for
     the longest pass count).
 
-Wait states are counted as issued instructions, s_nop N counting N + 1.  No GPU is
-needed: only the compiler's output is read.
+Wait states are counted as issued instructions, s_nop N counting N + 1.
+
+A second test reads the code object's kernel metadata and requires every kernel of
+the library to use no scratch memory (private segment size 0): a GEMM whose
+accumulators or fragment arrays land in scratch (an epilogue loop the compiler does
+not fully unroll indexes them dynamically) still computes the right result, but an
+order of magnitude slower.  No GPU is needed: only the compiler's output is read.
 """
 from __future__ import annotations
 
@@ -37,16 +42,25 @@ def _tool(name):
     return p if os.path.exists(p) else shutil.which(name)
 
 
-def _disassembly():
-    tools = [_tool(t) for t in ("llvm-objcopy", "clang-offload-bundler", "llvm-objdump")]
+def _code_object(d):
+    """The gfx950 code object of libsoklyn_hip.so, extracted into directory d."""
+    tools = [_tool(t) for t in ("llvm-objcopy", "clang-offload-bundler")]
     if not os.path.exists(LIB) or not all(tools):
         pytest.skip("libsoklyn_hip.so or the ROCm LLVM tools are not available")
-    objcopy, bundler, objdump = tools
+    objcopy, bundler = tools
+    fat, co = os.path.join(d, "fatbin.bin"), os.path.join(d, "co.o")
+    subprocess.run([objcopy, "--dump-section", f".hip_fatbin={fat}", LIB], check=True)
+    subprocess.run([bundler, "--type=o", "--targets=hipv4-amdgcn-amd-amdhsa--gfx950", f"--input={fat}",
+                    f"--output={co}", "--unbundle"], check=True)
+    return co
+
+
+def _disassembly():
+    objdump = _tool("llvm-objdump")
+    if not objdump:
+        pytest.skip("llvm-objdump is not available")
     with tempfile.TemporaryDirectory() as d:
-        fat, co = os.path.join(d, "fatbin.bin"), os.path.join(d, "co.o")
-        subprocess.run([objcopy, "--dump-section", f".hip_fatbin={fat}", LIB], check=True)
-        subprocess.run([bundler, "--type=o", "--targets=hipv4-amdgcn-amd-amdhsa--gfx950", f"--input={fat}",
-                        f"--output={co}", "--unbundle"], check=True)
+        co = _code_object(d)
         syms = sorted({m.group(0) for m in ONE_WAVE.finditer(
             subprocess.run([objdump, "-t", co], check=True, capture_output=True, text=True).stdout)
             if not m.group(0).endswith(".kd")})
@@ -96,3 +110,25 @@ def test_one_wave_kernels_keep_the_asm_mfma_hazard_invariants():
         reads = [i for i, s in enumerate(ins) if i > last and re.search(r"\ba(\d+|\[\d+:\d+\])", s)]
         assert reads, f"{name}: no epilogue read of the accumulators"
         assert _wait_states(ins[last + 1:reads[0]]) >= 19, f"{name}: epilogue reads AGPRs too soon after MFMA"
+
+
+def test_no_kernel_uses_scratch():
+    readelf = _tool("llvm-readelf")
+    if not readelf:
+        pytest.skip("llvm-readelf is not available")
+    with tempfile.TemporaryDirectory() as d:
+        notes = subprocess.run([readelf, "--notes", _code_object(d)], check=True, capture_output=True,
+                               text=True).stdout
+    sizes, name = {}, None
+    for line in notes.splitlines():
+        m = re.match(r"\s*\.name:\s+(\S+)", line)
+        if m:
+            name = m.group(1)
+        m = re.match(r"\s*\.private_segment_fixed_size:\s+(\d+)", line)
+        if m and name:
+            sizes[name] = int(m.group(1))
+            name = None
+    assert len(sizes) >= 20, f"kernel metadata not found ({len(sizes)} kernels)"
+    assert any("gemm_dma_kernel" in k for k in sizes)
+    bad = {k: v for k, v in sizes.items() if v}
+    assert not bad, f"kernels using scratch memory: {bad}"

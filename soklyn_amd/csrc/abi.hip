@@ -274,8 +274,6 @@ int32_t pad_keep(skl_ctx *ctx, const void *p, uint32_t rows, uint32_t cols, uint
     return SKL_OK;
 }
 
-size_t elem_size(uint32_t dtype) { return dtype == SKL_F16 ? 2 : 4; }
-
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // ---- GEMM planning ------------------------------------------------------------------
@@ -779,15 +777,20 @@ int32_t skl_ctx_create(int32_t ordinal, uint32_t tile_dim, skl_ctx **out) {
 
 int32_t skl_ctx_destroy(skl_ctx *ctx) {
     if (!ctx) return SKL_ERR_NULL_POINTER;
-    hipSetDevice(ctx->device);
-    hipStreamSynchronize(ctx->stream);
-    if (ctx->ws) hipFree(ctx->ws);
-    if (ctx->cols) hipFree(ctx->cols);
+    // every release is attempted; the first failure is reported
+    hipError_t first = hipSuccess;
+    auto note = [&](hipError_t e) {
+        if (first == hipSuccess && e != hipSuccess) first = e;
+    };
+    note(hipSetDevice(ctx->device));
+    note(hipStreamSynchronize(ctx->stream));
+    if (ctx->ws) note(hipFree(ctx->ws));
+    if (ctx->cols) note(hipFree(ctx->cols));
     for (PadCopy &c : ctx->pads)
-        if (c.buf) hipFree(c.buf);
-    hipStreamDestroy(ctx->own_stream);
+        if (c.buf) note(hipFree(c.buf));
+    note(hipStreamDestroy(ctx->own_stream));
     delete ctx;
-    return SKL_OK;
+    return first == hipSuccess ? SKL_OK : hip_status(first);
 }
 
 int32_t skl_ctx_set_sync(skl_ctx *ctx, uint32_t sync_each_call) {

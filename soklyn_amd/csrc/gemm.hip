@@ -421,7 +421,10 @@ template <typename T, int BM, int BN, int BK, int WM, int WN> struct Cfg {
 };
 typedef Cfg<half_t, 256, 256, 64, 2, 4> CfgH256w8;   // 8 waves, 128x64 per wave, 2 waves / SIMD
 typedef Cfg<half_t, 128, 128, 64, 2, 2> CfgH128;
-typedef Cfg<float, 128, 128, 32, 2, 2> CfgF128;
+// fp32: 8 waves of 64x32 on a 128x128 tile (two per SIMD hide each other's LDS and
+// barrier waits; C2 on 256 tiles, one workgroup per CU: dX 75.6 -> 72.0 us, step +2.3%
+// against 4 waves of 64x64)
+typedef Cfg<float, 128, 128, 32, 2, 4> CfgF128;
 typedef Cfg<float, 64, 64, 32, 2, 2> CfgF64;
 
 template <class C, bool AK, bool BK_, bool VOK, class Epi>

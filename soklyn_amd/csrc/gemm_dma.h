@@ -375,7 +375,12 @@ __global__ void __launch_bounds__(64 * NW)
 
     const uint32_t tid = threadIdx.x;
     const uint32_t lane = tid & 63u;
-    const uint32_t wave = tid >> 6;
+    // wave-uniform in an SGPR: every DMA's LDS destination (M0) is then scalar
+    // arithmetic; derived from the thread index it was a VGPR, read back with a
+    // v_readfirstlane before each DMA instruction, a VALU -> SGPR -> M0 chain that
+    // held the in-order wave off its next MFMA (one-wave-per-SIMD k-step with the
+    // refill: 1493 -> 1213 cycles per k-tile; C3 dX 205.5 -> 201.2 us)
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t wm = wave / C::WN, wn = wave % C::WN;
 
     uint32_t tm, tn;

@@ -246,11 +246,8 @@ struct Stager {
 // shapes are 4 tile rows x 8 tile columns, and its second round reuses the
 // same 4 A row panels from its L2 (2-4% faster than GROUP_M = 8 on the C3
 // forward and dX; 16 is slower).
-__device__ __forceinline__ void tile_coords(uint32_t wg, uint32_t tiles_m, uint32_t tiles_n, uint32_t &tm,
-                                            uint32_t &tn) {
-    const uint32_t total = tiles_m * tiles_n;
-    uint32_t t = wg;
-    if ((total & 7u) == 0) t = (wg & 7u) * (total >> 3) + (wg >> 3);
+__device__ __forceinline__ void tile_coords_grouped(uint32_t t, uint32_t tiles_m, uint32_t tiles_n, uint32_t &tm,
+                                                    uint32_t &tn) {
     constexpr uint32_t GROUP_M = 4;
     const uint32_t per_group = GROUP_M * tiles_n;
     const uint32_t group = t / per_group;
@@ -259,6 +256,13 @@ __device__ __forceinline__ void tile_coords(uint32_t wg, uint32_t tiles_m, uint3
     const uint32_t in_group = t - group * per_group;
     tm = first_m + in_group % gsize;
     tn = in_group / gsize;
+}
+__device__ __forceinline__ void tile_coords(uint32_t wg, uint32_t tiles_m, uint32_t tiles_n, uint32_t &tm,
+                                            uint32_t &tn) {
+    const uint32_t total = tiles_m * tiles_n;
+    uint32_t t = wg;
+    if ((total & 7u) == 0) t = (wg & 7u) * (total >> 3) + (wg >> 3);
+    tile_coords_grouped(t, tiles_m, tiles_n, tm, tn);
 }
 
 // The K loop: double-buffered LDS, register prefetch one K-tile ahead,

@@ -15,8 +15,8 @@ checks, for every such kernel, the invariants those wait states rely on:
 
 Wait states are counted as issued instructions, s_nop N counting N + 1.
 
-A second test reads the code object's kernel metadata and requires every kernel of
-the library to use no scratch memory (private segment size 0): a GEMM whose
+A second test reads the kernel metadata of every code object (one per source file)
+and requires every kernel of the library to use no scratch memory (private segment size 0): a GEMM whose
 accumulators or fragment arrays land in scratch (an epilogue loop the compiler does
 not fully unroll indexes them dynamically) still computes the right result, but an
 order of magnitude slower.  No GPU is needed: only the compiler's output is read.
@@ -42,42 +42,58 @@ def _tool(name):
     return p if os.path.exists(p) else shutil.which(name)
 
 
-def _code_object(d):
-    """The gfx950 code object of libsoklyn_hip.so, extracted into directory d."""
+def _code_objects(d):
+    """The gfx950 code objects of libsoklyn_hip.so (one offload bundle per source file in
+    its .hip_fatbin section), extracted into directory d."""
     tools = [_tool(t) for t in ("llvm-objcopy", "clang-offload-bundler")]
     if not os.path.exists(LIB) or not all(tools):
         pytest.skip("libsoklyn_hip.so or the ROCm LLVM tools are not available")
     objcopy, bundler = tools
-    fat, co = os.path.join(d, "fatbin.bin"), os.path.join(d, "co.o")
+    fat = os.path.join(d, "fatbin.bin")
     subprocess.run([objcopy, "--dump-section", f".hip_fatbin={fat}", LIB], check=True)
-    subprocess.run([bundler, "--type=o", "--targets=hipv4-amdgcn-amd-amdhsa--gfx950", f"--input={fat}",
-                    f"--output={co}", "--unbundle"], check=True)
-    return co
+    with open(fat, "rb") as f:
+        data = f.read()
+    magic = b"__CLANG_OFFLOAD_BUNDLE__"
+    starts, i = [], data.find(magic)
+    while i >= 0:
+        starts.append(i)
+        i = data.find(magic, i + 1)
+    cos = []
+    for k, a in enumerate(starts):
+        part, co = os.path.join(d, f"bundle{k}.bin"), os.path.join(d, f"co{k}.o")
+        with open(part, "wb") as f:
+            f.write(data[a:starts[k + 1] if k + 1 < len(starts) else len(data)])
+        subprocess.run([bundler, "--type=o", "--targets=hipv4-amdgcn-amd-amdhsa--gfx950", f"--input={part}",
+                        f"--output={co}", "--unbundle"], check=True)
+        cos.append(co)
+    assert cos, "no offload bundle in libsoklyn_hip.so"
+    return cos
 
 
 def _disassembly():
     objdump = _tool("llvm-objdump")
     if not objdump:
         pytest.skip("llvm-objdump is not available")
+    kernels = {}
     with tempfile.TemporaryDirectory() as d:
-        co = _code_object(d)
-        syms = sorted({m.group(0) for m in ONE_WAVE.finditer(
-            subprocess.run([objdump, "-t", co], check=True, capture_output=True, text=True).stdout)
-            if not m.group(0).endswith(".kd")})
-        if not syms:
-            return {}
-        out = subprocess.run([objdump, "-d", "--mcpu=gfx950", "--disassemble-symbols=" + ",".join(syms), co],
-                             check=True, capture_output=True, text=True).stdout
-    kernels, cur = {}, None
-    for line in out.splitlines():
-        m = re.match(r"^[0-9a-f]+ <(\S+)>:", line)
-        if m:
-            cur = m.group(1)
-            kernels[cur] = []
-        elif cur and line.startswith("\t"):
-            ins = line.strip().split("//")[0].strip()
-            if ins:
-                kernels[cur].append(ins)
+        for co in _code_objects(d):
+            syms = sorted({m.group(0) for m in ONE_WAVE.finditer(
+                subprocess.run([objdump, "-t", co], check=True, capture_output=True, text=True).stdout)
+                if not m.group(0).endswith(".kd")})
+            if not syms:
+                continue
+            out = subprocess.run([objdump, "-d", "--mcpu=gfx950", "--disassemble-symbols=" + ",".join(syms), co],
+                                 check=True, capture_output=True, text=True).stdout
+            cur = None
+            for line in out.splitlines():
+                m = re.match(r"^[0-9a-f]+ <(\S+)>:", line)
+                if m:
+                    cur = m.group(1)
+                    kernels[cur] = []
+                elif cur and line.startswith("\t"):
+                    ins = line.strip().split("//")[0].strip()
+                    if ins:
+                        kernels[cur].append(ins)
     return kernels
 
 
@@ -116,19 +132,21 @@ def test_no_kernel_uses_scratch():
     readelf = _tool("llvm-readelf")
     if not readelf:
         pytest.skip("llvm-readelf is not available")
+    sizes = {}
     with tempfile.TemporaryDirectory() as d:
-        notes = subprocess.run([readelf, "--notes", _code_object(d)], check=True, capture_output=True,
-                               text=True).stdout
-    sizes, name = {}, None
-    for line in notes.splitlines():
-        m = re.match(r"\s*\.name:\s+(\S+)", line)
-        if m:
-            name = m.group(1)
-        m = re.match(r"\s*\.private_segment_fixed_size:\s+(\d+)", line)
-        if m and name:
-            sizes[name] = int(m.group(1))
+        for co in _code_objects(d):
+            notes = subprocess.run([readelf, "--notes", co], check=True, capture_output=True, text=True).stdout
             name = None
+            for line in notes.splitlines():
+                m = re.match(r"\s*\.name:\s+(\S+)", line)
+                if m:
+                    name = m.group(1)
+                m = re.match(r"\s*\.private_segment_fixed_size:\s+(\d+)", line)
+                if m and name:
+                    sizes[name] = int(m.group(1))
+                    name = None
     assert len(sizes) >= 20, f"kernel metadata not found ({len(sizes)} kernels)"
     assert any("gemm_dma_kernel" in k for k in sizes)
+    assert any("error_flat_kernel" in k for k in sizes) and any("norm_rows" in k for k in sizes)
     bad = {k: v for k, v in sizes.items() if v}
     assert not bad, f"kernels using scratch memory: {bad}"

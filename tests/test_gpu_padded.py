@@ -124,6 +124,11 @@ def test_input_grad_row_band(ctx):
     (6000, 1000, 1531, 2),   # 24 padded tiles: split-K over the batch, partial planes reduced
     (2048, 2048, 2048, 0),   # 64 whole tiles, operands read in place: split-K only
     (300, 4000, 3001, 1),    # 192 padded tiles, no split: Adam in the element-wise epilogue
+    # split-K grids whose (tile, slice) count is not a multiple of 8 keep the tile order
+    # (the others are remapped onto the XCDs): 49 tiles x 5 slices on 256x256 ...
+    (5632, 1792, 1792, 1),
+    # ... and 36 128x128 tiles x 11 slices
+    (5632, 768, 768, 2),
 ])
 def test_backward_padded_and_split(ctx, M, K, N, norm):
     print(f"backward {M}: {K}x{N} norm {norm}", flush=True)
